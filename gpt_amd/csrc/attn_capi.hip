@@ -1,0 +1,128 @@
+// C ABI of the gfx950 causal-attention backend (declared in
+// include/gpt_hip_attn.h): argument validation, kernel selection, status codes.
+//
+// The reference's op methods return void and abort on any runtime error
+// (src/backend/cuda/utils/cuda_utils.cuh:21-34, 64-77); here every entry point
+// returns a status and keeps a per-thread message, and the reference-side
+// adapter turns a non-zero status back into print + abort.
+#include "../../include/gpt_hip_attn.h"
+#include "attn_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+namespace {
+
+thread_local char g_err[512] = "";
+int g_path = 0;  // 0 automatic, 1 general-d kernels only
+
+int fail(int code, const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_shape(const char *op, int B, int T, int C, int H, gpt_attn::Shape *s)
+{
+    if (B < 0 || T < 0 || C <= 0 || H <= 0)
+        return fail(GPT_HIP_ATTN_EINVAL, "%s: invalid shape B=%d T=%d C=%d H=%d", op, B, T, C, H);
+    if (C % H != 0)
+        return fail(GPT_HIP_ATTN_EINVAL, "%s: hidden_size %d is not a multiple of num_heads %d", op, C, H);
+    const int d = C / H;
+    if (d > 256)
+        return fail(GPT_HIP_ATTN_EHEADDIM, "%s: head_dim %d is not supported (1..256)", op, d);
+    // Element offsets are computed in 64-bit; the grid uses one block per
+    // (tile, b, h) or per 128 rows, which must fit a 32-bit grid dimension.
+    const long long rows = (long long)B * T * H;
+    if ((long long)B * T * 3LL * C >= (1LL << 40) || rows >= (1LL << 31))
+        return fail(GPT_HIP_ATTN_ERANGE, "%s: tensor too large (B=%d T=%d C=%d)", op, B, T, C);
+    *s = gpt_attn::Shape{B, T, C, H, d};
+    return 0;
+}
+
+int check_device(const char *op)
+{
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0)
+        return fail(GPT_HIP_ATTN_ENODEV, "%s: no HIP device (%s)", op,
+                    e != hipSuccess ? hipGetErrorString(e) : "device count is 0");
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gpt_hip_attn_fwd_f32(float *y, float *lse, const float *qkv, int batch_size, int seq_len,
+                         int hidden_size, int num_heads, void *stream)
+{
+    static const char *op = "gpt_hip_attn_fwd_f32";
+    gpt_attn::Shape s;
+    if (int rc = check_shape(op, batch_size, seq_len, hidden_size, num_heads, &s))
+        return rc;
+    if (batch_size == 0 || seq_len == 0)
+        return 0;
+    if (!y || !lse || !qkv)
+        return fail(GPT_HIP_ATTN_ENULL, "%s: NULL tensor pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool mfma = g_path == 0 && s.d == 64 && aligned16(y) && aligned16(qkv);
+    const hipError_t e = mfma ? gpt_attn::launch_fwd_d64(y, lse, qkv, s, st)
+                              : gpt_attn::launch_fwd_general(y, lse, qkv, s, st);
+    if (e != hipSuccess)
+        return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
+    return 0;
+}
+
+int gpt_hip_attn_bwd_f32(float *grad_x, float *D_cache, const float *lse, const float *grad_y,
+                         const float *y, const float *qkv, int batch_size, int seq_len, int hidden_size,
+                         int num_heads, void *stream)
+{
+    static const char *op = "gpt_hip_attn_bwd_f32";
+    gpt_attn::Shape s;
+    if (int rc = check_shape(op, batch_size, seq_len, hidden_size, num_heads, &s))
+        return rc;
+    if (batch_size == 0 || seq_len == 0)
+        return 0;
+    if (!grad_x || !D_cache || !lse || !grad_y || !y || !qkv)
+        return fail(GPT_HIP_ATTN_ENULL, "%s: NULL tensor pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool mfma = g_path == 0 && s.d == 64 && aligned16(grad_x) && aligned16(grad_y) && aligned16(y) &&
+                      aligned16(qkv);
+    const hipError_t e = mfma ? gpt_attn::launch_bwd_d64(grad_x, D_cache, lse, grad_y, y, qkv, s, st)
+                              : gpt_attn::launch_bwd_general(grad_x, D_cache, lse, grad_y, y, qkv, s, st);
+    if (e != hipSuccess)
+        return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
+    return 0;
+}
+
+const char *gpt_hip_attn_last_error(void) { return g_err; }
+
+int gpt_hip_attn_device_ok(void)
+{
+    int n = 0;
+    return hipGetDeviceCount(&n) == hipSuccess && n > 0 ? 1 : 0;
+}
+
+int gpt_hip_attn_set_path(int path)
+{
+    if (path != 0 && path != 1)
+        return fail(GPT_HIP_ATTN_EINVAL, "gpt_hip_attn_set_path: unknown path %d", path);
+    const int prev = g_path;
+    g_path = path;
+    return prev;
+}
+
+}  // extern "C"

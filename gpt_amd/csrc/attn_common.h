@@ -1,0 +1,54 @@
+// Shared definitions for the gfx950 causal-attention kernels.
+//
+// Tensor layouts are the reference's (src/backend/backend_interface.h:161-184):
+//   qkv [B, T, 3C] (Q | K | V, head h at column h*d of each third),
+//   y [B, T, C], lse / D [B, T, H], grad_x [B, T, 3C].
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gpt_attn {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// LDS row stride (floats) for 64-wide fp32 tiles. gfx950's LDS serves b32 and
+// b128 reads as 32 banks x 4 bytes (measured with a stride sweep); a stride of
+// 64 + 4 words puts the 8 lanes of one b128 phase, each reading its own row,
+// on 8 disjoint 4-bank groups, and keeps half-wave b32/b64 row reads linear.
+constexpr int kRowStride = 68;
+
+// v_mfma_f32_32x32x2_f32: D[32x32] += A[32x2] * B[2x32].
+// Lane l supplies A[l%32][l/32] and B[l/32][l%32]; it holds accumulator
+// element D[row(r, l/32)][l%32] in register r (see mfma_row).
+__device__ __forceinline__ v16f mfma32(float a, float b, v16f c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Row index of accumulator register r for a lane in half `hf` (= lane / 32).
+__device__ __forceinline__ constexpr int mfma_row(int r, int hf)
+{
+    return 8 * (r >> 2) + 4 * hf + (r & 3);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// Value held by lane l ^ 32 (the other half of the wave64).
+__device__ __forceinline__ float swap_halves(float x) { return __shfl_xor(x, 32, 64); }
+
+__device__ __forceinline__ v16f zero16()
+{
+    v16f z;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        z[i] = 0.f;
+    return z;
+}
+
+}  // namespace gpt_attn

@@ -1,0 +1,91 @@
+/*
+ * gpt_hip_attn.h - C ABI of the MI355X (gfx950) causal self-attention backend.
+ *
+ * This is the drop-in boundary for the reference's attention op pair. The
+ * reference exposes it as two virtual methods of its op-level interface
+ * IGPTBackend; a backend adapter implements each method by calling the entry
+ * point below with the same arguments in the same order (plus a stream).
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor pointers are DEVICE pointers (hipMalloc'd or equivalent),
+ *     fp32, C-contiguous, in the reference's layouts:
+ *       qkv     [B, T, 3C]  Q | K | V; head h occupies columns h*d .. h*d+d-1
+ *                           of each third, d = C / H
+ *       y       [B, T, C]
+ *       lse     [B, T, H]   token-major, natural log, of the scaled scores
+ *       grad_y  [B, T, C]
+ *       grad_x  [B, T, 3C]  dQ | dK | dV
+ *       D_cache [B, T, H]
+ *   - Softmax scale is 1/sqrt(d); the causal mask keeps key j <= query i.
+ *   - `stream` is a hipStream_t passed as void*; NULL means the default stream.
+ *     Work is enqueued asynchronously; nothing is allocated on the device.
+ *   - Return 0 on success or a negative GPT_HIP_ATTN_E* code; the message of
+ *     the last failure on the calling thread is kept for
+ *     gpt_hip_attn_last_error(). Inputs are never modified.
+ *   - B == 0 or T == 0 is a successful no-op.
+ *   - head_dim 64 runs the fp32-MFMA kernels (pointers must be 16-byte
+ *     aligned, which the reference's 4-float tensor padding guarantees);
+ *     any other head_dim in 1..256, or a misaligned pointer, runs the
+ *     general-d HIP kernels.
+ */
+#ifndef GPT_HIP_ATTN_H
+#define GPT_HIP_ATTN_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GPT_HIP_ATTN_OK 0
+#define GPT_HIP_ATTN_EINVAL (-1)     /* bad shape: B,T < 0, C,H <= 0, C % H != 0 */
+#define GPT_HIP_ATTN_ENULL (-2)      /* a required pointer is NULL */
+#define GPT_HIP_ATTN_EHEADDIM (-3)   /* head_dim outside 1..256 */
+#define GPT_HIP_ATTN_ENODEV (-4)     /* no usable HIP device */
+#define GPT_HIP_ATTN_ELAUNCH (-5)    /* a kernel launch failed */
+#define GPT_HIP_ATTN_ERANGE (-6)     /* tensor too large for the index types */
+
+/* Causal attention forward: writes every element of y and lse.
+ * Replaces IGPTBackend::device_flash_attention_forward
+ * (reference src/backend/backend_interface.h:161-170; CUDA implementation
+ * src/backend/cuda/kernels/attention.cu:249-268; CPU oracle
+ * src/backend/cpu/cpu_backend.cpp:289-356). Same argument order. */
+int gpt_hip_attn_fwd_f32(float *y, float *lse, const float *qkv,
+                         int batch_size, int seq_len, int hidden_size, int num_heads,
+                         void *stream);
+
+/* Causal attention backward: OVERWRITES grad_x with dQ | dK | dV and writes
+ * D_cache[b,t,h] = sum_d grad_y * y. `lse` and `y` are the forward's outputs.
+ * Replaces IGPTBackend::device_flash_attention_backward
+ * (reference src/backend/backend_interface.h:172-184; CUDA implementation
+ * src/backend/cuda/kernels/attention.cu:545-577; CPU oracle
+ * src/backend/cpu/cpu_backend.cpp:358-437). Same argument order. */
+int gpt_hip_attn_bwd_f32(float *grad_x, float *D_cache, const float *lse,
+                         const float *grad_y, const float *y, const float *qkv,
+                         int batch_size, int seq_len, int hidden_size, int num_heads,
+                         void *stream);
+
+/* Message for the last non-zero return on the calling thread ("" if none).
+ * No reference counterpart: the reference prints and aborts instead
+ * (src/backend/cuda/utils/cuda_utils.cuh:21-34); adapters that keep that
+ * behaviour print this string before abort(). */
+const char *gpt_hip_attn_last_error(void);
+
+/* 1 if a HIP device is present and usable, else 0. No reference counterpart
+ * (the reference assumes a device). */
+int gpt_hip_attn_device_ok(void);
+
+/* Kernel selection, for tests and tuning only (not thread-safe; process-wide).
+ *   path 0  automatic (default): MFMA kernels for head_dim 64, general-d
+ *           kernels otherwise
+ *   path 1  always the general-d kernels (a second, independent HIP
+ *           implementation used to cross-check the MFMA kernels)
+ * Returns the previous path, or GPT_HIP_ATTN_EINVAL for an unknown path.
+ * No reference counterpart. */
+int gpt_hip_attn_set_path(int path);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GPT_HIP_ATTN_H */
