@@ -145,8 +145,9 @@ def device_ok() -> bool:
 
 
 def set_path(path: int) -> int:
-    """0 = automatic (MFMA kernels for head_dim 64), 1 = general-d kernels only.
-    Returns the previous setting. Test hook; process-wide."""
+    """0 = automatic (MFMA kernels for head_dim 64, deterministic backward),
+    1 = general-d kernels only, 2 = as 0 but with the fp32-atomic dQ backward.
+    Returns the previous setting. Test and tuning hook; process-wide."""
     rc = load_library().gpt_hip_attn_set_path(path)
     if rc < 0:
         _check(rc)

@@ -9,25 +9,28 @@
 //   dQ_i  = sum_j dS_ij k_j,  dK_j = sum_i dS_ij q_i,  dV_j = sum_i P_ij dO_i
 // grad_x is overwritten (dQ | dK | dV in the qkv layout) and D is written.
 //
-// head_dim 64 path, two launches:
-//   bwd_prep_kernel  D rows, and zeroes the dQ third of grad_x
-//   bwd_d64_kernel   one workgroup of NW = 2*QS waves owns BKV = 32*NW keys and
-//                    walks the query blocks (BQ = 32*QS rows) from its diagonal
-//                    to T. Each wave keeps its 32 keys' K and V as MFMA
-//                    operands in registers and accumulates dK, dV in
-//                    registers (written once, with plain stores, at the end).
-//                    Per query block:
-//                      S  = Q K^T, dP = dO V^T        (queries x keys)
-//                      dV += P^T dO, dK += dS^T Q     (accumulators of S/dP
-//                                                      are used directly as
-//                                                      the A operand)
-//                      dS -> LDS; after a barrier every wave computes one
-//                      32x32 tile of dQ = dS K over all BKV keys of the
-//                      workgroup and adds it to grad_x with fp32 atomics.
-//                    The LDS round trip transposes dS into the A layout and
-//                    reduces the NW waves' key ranges before anything touches
-//                    global memory, so each workgroup issues one atomic per
-//                    dQ element per query block.
+// head_dim 64 path: deterministic, three launches, no atomics, no memset.
+// Work unit = one 32-query block i x one 32-key block j with j <= i.
+//   bwd_rowdot_d64_kernel  D rows; one wave per token row, 16 lanes per head.
+//   bwd_dkdv_d64_kernel    one workgroup per (b, h, key block j); its NW waves
+//                          split the query blocks i >= j (wave w takes
+//                          j + w, j + w + NW, ...). Per unit, on
+//                          v_mfma_f32_32x32x2_f32:
+//                            S  = Q K^T, dP = dO V^T   (queries x keys)
+//                            P = 2^(S c - L), dS = P (dP - D)
+//                            dV += P^T dO, dK += dS^T Q (the S / dP
+//                              accumulators are the A operands as they are)
+//                          and the dS tile is stored to a workspace. The NW
+//                          partial dK, dV are summed through LDS in a fixed
+//                          order and written once with plain stores.
+//   bwd_dq_d64_kernel      one wave per (b, h, query block i):
+//                          dQ_i = sum_{j<=i} dS_ij K_j from the workspace,
+//                          written once with plain stores.
+// Materialising dS costs 4 KiB of workspace per unit (28 MiB per layer at
+// B=16, T=256, H=12), written and read once; in exchange no dQ element is
+// accumulated by more than one wave, the result is bitwise reproducible, and
+// the dK/dV and dQ work both split into units small enough to balance the
+// causal triangle over 256 CUs. The atomic alternative is attn_bwd_atomic.hip.
 #include "attn_common.h"
 #include "attn_kernels.h"
 
@@ -35,8 +38,9 @@
 
 namespace gpt_attn {
 
-// D[b,t,h] = sum_e dO*O over the head's d columns; optionally zero the dQ
-// third of grad_x for the same (b, t, h) slice. One thread per (b, t, h).
+// D[b,t,h] = sum_e dO*O over the head's d columns, any head_dim; optionally
+// zero the dQ third of grad_x for the same (b, t, h) slice (used by the atomic
+// variant). One thread per (b, t, h).
 __global__ __launch_bounds__(256) void bwd_prep_kernel(float *__restrict__ grad_x,
                                                        float *__restrict__ Dout,
                                                        const float *__restrict__ dy,
@@ -87,211 +91,251 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(float *__restrict__ grad_
     }
 }
 
-template <int QS>
-__global__ __launch_bounds__(128 * QS) void bwd_d64_kernel(float *__restrict__ grad_x,
-                                                           const float *__restrict__ lse,
-                                                           const float *__restrict__ Dv,
-                                                           const float *__restrict__ dy,
-                                                           const float *__restrict__ qkv,
-                                                           int B, int T, int C, int H,
-                                                           float scale, float c2)
+// D rows for head_dim 64: one wave per token row (all H heads), lane l reads
+// float4s l, l + 64, ... of the row; the 16 lanes of one head sum their
+// products in 4 butterfly steps.
+__global__ __launch_bounds__(256) void bwd_rowdot_d64_kernel(float *__restrict__ Dout,
+                                                             const float *__restrict__ dy,
+                                                             const float *__restrict__ y,
+                                                             long rows, int H)
 {
-    constexpr int NW = 2 * QS, NT = NW * 64, BKV = 32 * NW, BQ = 32 * QS;
-    constexpr int ST = kRowStride, DSST = BKV + 4;  // both = 4 (mod 32) words
-    __shared__ __attribute__((aligned(16))) float k_lds[BKV * ST];   // keys of the workgroup
-    __shared__ __attribute__((aligned(16))) float q_lds[BQ * ST];    // Q of the query block
-    __shared__ __attribute__((aligned(16))) float o_lds[BQ * ST];    // dO of the query block
-    __shared__ __attribute__((aligned(16))) float s_lds[BQ * DSST];  // dS (queries x keys)
-    __shared__ __attribute__((aligned(16))) float l_lds[BQ];         // lse * log2(e)
-    __shared__ __attribute__((aligned(16))) float d_lds[BQ];         // D
+    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows)
+        return;
+    const int lane = threadIdx.x & 63;
+    const long C = 64L * H;
+    const float4 *a = reinterpret_cast<const float4 *>(dy + row * C);
+    const float4 *o = reinterpret_cast<const float4 *>(y + row * C);
+    for (int f = lane; f < 16 * H; f += 64)  // uniform within each 16-lane group
+    {
+        const float4 u = a[f], v = o[f];
+        float s = u.x * v.x + u.y * v.y + u.z * v.z + u.w * v.w;
+        s += __shfl_xor(s, 8, 16);
+        s += __shfl_xor(s, 4, 16);
+        s += __shfl_xor(s, 2, 16);
+        s += __shfl_xor(s, 1, 16);
+        if ((lane & 15) == 0)
+            Dout[row * H + (f >> 4)] = s;
+    }
+}
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+// Offset (floats) of dS tile (i, j), j <= i, inside one (b, h)'s workspace.
+__device__ __forceinline__ long ds_tile(int i, int j) { return ((long)i * (i + 1) / 2 + j) * 1024; }
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void bwd_dkdv_d64_kernel(float *__restrict__ grad_x,
+                                                               float *__restrict__ dsw,
+                                                               const float *__restrict__ lse,
+                                                               const float *__restrict__ Dv,
+                                                               const float *__restrict__ dy,
+                                                               const float *__restrict__ qkv,
+                                                               int T, int C, int H, int bh0, int BHc,
+                                                               int n_qb, float c2, float scale)
+{
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int n = lane & 31, hf = lane >> 5;
-    const int BH = B * H;
-    // Key block 0 sees every query block: lowest key blocks go first.
-    const int kb = (int)(blockIdx.x / BH);
-    const int bh = blockIdx.x % BH;
+    // key block j, lowest first (it has the most query blocks)
+    const int j = (int)(blockIdx.x / BHc);
+    const int bhl = (int)(blockIdx.x % BHc), bh = bh0 + bhl;
     const int b = bh / H, h = bh % H;
     const long W = 3L * C;
-    const float *qb = qkv + (long)b * T * W + (long)h * 64;
+    const float *qb_ = qkv + (long)b * T * W + (long)h * 64;
     const float *dob = dy + (long)b * T * C + (long)h * 64;
     const float *lb = lse + (long)b * T * H + h;
-    const float *db_ = Dv + (long)b * T * H + h;
-    float *gq = grad_x + (long)b * T * W + (long)h * 64;
-    const int kb0 = kb * BKV;
-    const int kw = kb0 + 32 * w;  // first key of this wave
+    const float *db = Dv + (long)b * T * H + h;
+    float *ws = dsw + (long)bhl * ((long)n_qb * (n_qb + 1) / 2) * 1024;
+    const int k0 = 32 * j;
 
     // B operands of S = Q K^T and dP = dO V^T: lane (n, hf) holds
-    // K[kw+n][32hf + s] and V[kw+n][32hf + s], s = 0..31.
-    float kop[32], vop[32];
+    // K[k0 + n][32 hf + s] and V[k0 + n][32 hf + s]. Keys at or beyond T are
+    // read from row T - 1; they only meet masked (query < key) entries.
+    float4 kop[8], vop[8];
     {
-        const int key = kw + n;
-        if (key < T)
+        const float *src = qb_ + (long)min(k0 + n, T - 1) * W + 32 * hf;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
         {
-            const float4 *ks = reinterpret_cast<const float4 *>(qb + (long)key * W + C + 32 * hf);
-            const float4 *vs = reinterpret_cast<const float4 *>(qb + (long)key * W + 2 * C + 32 * hf);
+            kop[t] = reinterpret_cast<const float4 *>(src + C)[t];
+            vop[t] = reinterpret_cast<const float4 *>(src + 2 * C)[t];
+        }
+    }
+
+    __shared__ __attribute__((aligned(16))) float sm_ld[NW][2][32];  // per wave: L * log2(e), D
+    v16f dk0 = zero16(), dk1 = zero16(), dv0 = zero16(), dv1 = zero16();
+
+    for (int i = j + w; i < n_qb; i += NW)
+    {
+        const int q0 = 32 * i;
+        const int qr = min(q0 + n, T - 1);
+        if (hf == 0)
+        {
+            sm_ld[w][0][n] = lb[(long)qr * H] * kLog2e;
+            sm_ld[w][1][n] = db[(long)qr * H];
+        }
+        // S[query q0 + row(r)][key k0 + n] and dP likewise; A operands
+        // Q[q0 + n][32 hf + s] and dO[q0 + n][32 hf + s].
+        v16f s = zero16(), dp = zero16();
+        {
+            const float4 *qs = reinterpret_cast<const float4 *>(qb_ + (long)qr * W + 32 * hf);
+            const float4 *os = reinterpret_cast<const float4 *>(dob + (long)qr * C + 32 * hf);
 #pragma unroll
             for (int t = 0; t < 8; ++t)
             {
-                const float4 a = ks[t], v = vs[t];
-                kop[4 * t + 0] = a.x;
-                kop[4 * t + 1] = a.y;
-                kop[4 * t + 2] = a.z;
-                kop[4 * t + 3] = a.w;
-                vop[4 * t + 0] = v.x;
-                vop[4 * t + 1] = v.y;
-                vop[4 * t + 2] = v.z;
-                vop[4 * t + 3] = v.w;
+                const float4 qa = qs[t], oa = os[t];
+                s = mfma32(qa.x, kop[t].x, s);
+                dp = mfma32(oa.x, vop[t].x, dp);
+                s = mfma32(qa.y, kop[t].y, s);
+                dp = mfma32(oa.y, vop[t].y, dp);
+                s = mfma32(qa.z, kop[t].z, s);
+                dp = mfma32(oa.z, vop[t].z, dp);
+                s = mfma32(qa.w, kop[t].w, s);
+                dp = mfma32(oa.w, vop[t].w, dp);
             }
         }
-        else
-        {
+        wave_lds_sync();
+        // P and dS (without the 1/sqrt(d)); zero where key > query or the
+        // query row is past T.
 #pragma unroll
-            for (int s = 0; s < 32; ++s)
-                kop[s] = vop[s] = 0.f;
-        }
-    }
-    // K of all BKV keys, row-major, for the B operand of dQ = dS K.
-    for (int idx = tid; idx < BKV * 16; idx += NT)
-    {
-        const int r = idx >> 4, c4 = (idx & 15) * 4, key = kb0 + r;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (key < T)
-            v = *reinterpret_cast<const float4 *>(qb + (long)key * W + C + c4);
-        *reinterpret_cast<float4 *>(&k_lds[r * ST + c4]) = v;
-    }
-
-    v16f dk0 = zero16(), dk1 = zero16(), dv0 = zero16(), dv1 = zero16();
-
-    for (int q0 = kb0; q0 < T; q0 += BQ)
-    {
-        __syncthreads();  // previous block's LDS reads are done
-        for (int idx = tid; idx < BQ * 16; idx += NT)
+        for (int g = 0; g < 4; ++g)
         {
-            const int r = idx >> 4, c4 = (idx & 15) * 4, row = q0 + r;
-            float4 qv = make_float4(0.f, 0.f, 0.f, 0.f), ov = qv;
-            if (row < T)
+            const float4 l4 = *reinterpret_cast<const float4 *>(&sm_ld[w][0][8 * g + 4 * hf]);
+            const float4 d4 = *reinterpret_cast<const float4 *>(&sm_ld[w][1][8 * g + 4 * hf]);
+            const float lj[4] = {l4.x, l4.y, l4.z, l4.w};
+            const float dj[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
             {
-                qv = *reinterpret_cast<const float4 *>(qb + (long)row * W + c4);
-                ov = *reinterpret_cast<const float4 *>(dob + (long)row * C + c4);
-            }
-            *reinterpret_cast<float4 *>(&q_lds[r * ST + c4]) = qv;
-            *reinterpret_cast<float4 *>(&o_lds[r * ST + c4]) = ov;
-        }
-        if (tid < BQ)
-        {
-            const int row = q0 + tid;
-            l_lds[tid] = row < T ? lb[(long)row * H] * kLog2e : 0.f;
-            d_lds[tid] = row < T ? db_[(long)row * H] : 0.f;
-        }
-        __syncthreads();
-
-#pragma unroll
-        for (int sb = 0; sb < QS; ++sb)
-        {
-            const int qs0 = q0 + 32 * sb;  // first query of the sub-block
-            if (kw <= qs0 + 31)
-            {
-                // S[query qs0 + row(r)][key kw + n] and dP likewise.
-                v16f s = zero16(), dp = zero16();
-                const float *qr = &q_lds[(32 * sb + n) * ST + 32 * hf];
-                const float *orow = &o_lds[(32 * sb + n) * ST + 32 * hf];
-#pragma unroll
-                for (int t = 0; t < 8; ++t)
-                {
-                    const float4 qv = *reinterpret_cast<const float4 *>(qr + 4 * t);
-                    const float4 ov = *reinterpret_cast<const float4 *>(orow + 4 * t);
-                    s = mfma32(qv.x, kop[4 * t + 0], s);
-                    dp = mfma32(ov.x, vop[4 * t + 0], dp);
-                    s = mfma32(qv.y, kop[4 * t + 1], s);
-                    dp = mfma32(ov.y, vop[4 * t + 1], dp);
-                    s = mfma32(qv.z, kop[4 * t + 2], s);
-                    dp = mfma32(ov.z, vop[4 * t + 2], dp);
-                    s = mfma32(qv.w, kop[4 * t + 3], s);
-                    dp = mfma32(ov.w, vop[4 * t + 3], dp);
-                }
-                const bool diag = kw + 31 > qs0;
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-                {
-                    const float4 lv = *reinterpret_cast<const float4 *>(&l_lds[32 * sb + 8 * g + 4 * hf]);
-                    const float4 dv = *reinterpret_cast<const float4 *>(&d_lds[32 * sb + 8 * g + 4 * hf]);
-                    const float lj[4] = {lv.x, lv.y, lv.z, lv.w};
-                    const float dj[4] = {dv.x, dv.y, dv.z, dv.w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                    {
-                        const int r = 4 * g + j;
-                        float p = fast_exp2(s[r] * c2 - lj[j]);
-                        if (diag && kw + n > qs0 + 8 * g + 4 * hf + j)
-                            p = 0.f;
-                        s[r] = p;
-                        dp[r] = p * (dp[r] - dj[j]);  // dS without the 1/sqrt(d)
-                    }
-                }
-                // dV += P^T dO and dK += dS^T Q; step st contracts query
-                // qs0 + row(st, hf), the query of accumulator register st.
-#pragma unroll
-                for (int st = 0; st < 16; ++st)
-                {
-                    const int rr = 32 * sb + mfma_row(st, hf);
-                    const float2 g = *reinterpret_cast<const float2 *>(&o_lds[rr * ST + 2 * n]);
-                    const float2 qq = *reinterpret_cast<const float2 *>(&q_lds[rr * ST + 2 * n]);
-                    dv0 = mfma32(s[st], g.x, dv0);
-                    dv1 = mfma32(s[st], g.y, dv1);
-                    dk0 = mfma32(dp[st], qq.x, dk0);
-                    dk1 = mfma32(dp[st], qq.y, dk1);
-                }
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    s_lds[(32 * sb + mfma_row(r, hf)) * DSST + 32 * w + n] = dp[r];
-            }
-            else
-            {
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    s_lds[(32 * sb + mfma_row(r, hf)) * DSST + 32 * w + n] = 0.f;
+                const int r = 4 * g + jj;
+                const int qrow = q0 + 8 * g + 4 * hf + jj;  // = q0 + row(r, hf)
+                const bool keep = (k0 + n <= qrow) && (qrow < T);
+                const float p = fast_exp2(s[r] * c2 - lj[jj]);
+                s[r] = keep ? p : 0.f;
+                dp[r] = keep ? p * (dp[r] - dj[jj]) : 0.f;
             }
         }
-        __syncthreads();
-
-        // dQ tile (query sub-block w/2, dims 32*(w%2) .. +31) over all BKV keys.
+        // dS tile, query-major (row = query, column = key).
         {
-            const int sbq = w >> 1, dblk = w & 1;
-            v16f acc = zero16();
-            const float *arow = &s_lds[(32 * sbq + n) * DSST + hf * (BKV / 2)];
-            const float *bcol = &k_lds[(hf * (BKV / 2)) * ST + 32 * dblk + n];
-#pragma unroll
-            for (int t = 0; t < BKV / 8; ++t)
-            {
-                const float4 a = *reinterpret_cast<const float4 *>(arow + 4 * t);
-                acc = mfma32(a.x, bcol[(4 * t + 0) * ST], acc);
-                acc = mfma32(a.y, bcol[(4 * t + 1) * ST], acc);
-                acc = mfma32(a.z, bcol[(4 * t + 2) * ST], acc);
-                acc = mfma32(a.w, bcol[(4 * t + 3) * ST], acc);
-            }
+            float *tile = ws + ds_tile(i, j);
 #pragma unroll
             for (int r = 0; r < 16; ++r)
+                tile[mfma_row(r, hf) * 32 + n] = dp[r];
+        }
+        // dV += P^T dO and dK += dS^T Q; step st contracts query
+        // q0 + row(st, hf), the query of accumulator register st. B operands
+        // dO / Q[q0 + row(st, hf)][2n, 2n + 1].
+#pragma unroll
+        for (int st = 0; st < 16; ++st)
+        {
+            const long rr = min(q0 + mfma_row(st, hf), T - 1);
+            const float2 g2 = *reinterpret_cast<const float2 *>(dob + rr * C + 2 * n);
+            const float2 q2 = *reinterpret_cast<const float2 *>(qb_ + rr * W + 2 * n);
+            dv0 = mfma32(s[st], g2.x, dv0);
+            dv1 = mfma32(s[st], g2.y, dv1);
+            dk0 = mfma32(dp[st], q2.x, dk0);
+            dk1 = mfma32(dp[st], q2.y, dk1);
+        }
+        wave_lds_sync();
+    }
+
+    // Sum the NW partial dK / dV in wave order and store. Register r of lane
+    // (n, hf) holds key k0 + row(r, hf), dims 2n (dk0, dv0) and 2n + 1.
+    constexpr int RPW = 16 / NW;  // registers finished by each wave
+    if constexpr (NW > 1)
+    {
+        __shared__ float sm_red[NW][64][64];  // [wave][value][lane]
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+        {
+            sm_red[w][r][lane] = dk0[r];
+            sm_red[w][16 + r][lane] = dk1[r];
+            sm_red[w][32 + r][lane] = dv0[r];
+            sm_red[w][48 + r][lane] = dv1[r];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < RPW; ++u)
+        {
+            const int r = w * RPW + u;
+            float a0 = 0.f, a1 = 0.f, c0 = 0.f, c1 = 0.f;
+#pragma unroll
+            for (int v = 0; v < NW; ++v)
             {
-                const int row = q0 + 32 * sbq + mfma_row(r, hf);
-                if (row < T)
-                    unsafeAtomicAdd(&gq[(long)row * W + 32 * dblk + n], acc[r] * scale);
+                a0 += sm_red[v][r][lane];
+                a1 += sm_red[v][16 + r][lane];
+                c0 += sm_red[v][32 + r][lane];
+                c1 += sm_red[v][48 + r][lane];
+            }
+            const int key = k0 + mfma_row(r, hf);
+            if (key < T)
+            {
+                float *dst = grad_x + ((long)b * T + key) * W + (long)h * 64 + 2 * n;
+                *reinterpret_cast<float2 *>(dst + C) = make_float2(a0 * scale, a1 * scale);
+                *reinterpret_cast<float2 *>(dst + 2 * C) = make_float2(c0, c1);
             }
         }
     }
+    else
+    {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+        {
+            const int key = k0 + mfma_row(r, hf);
+            if (key < T)
+            {
+                float *dst = grad_x + ((long)b * T + key) * W + (long)h * 64 + 2 * n;
+                *reinterpret_cast<float2 *>(dst + C) = make_float2(dk0[r] * scale, dk1[r] * scale);
+                *reinterpret_cast<float2 *>(dst + 2 * C) = make_float2(dv0[r], dv1[r]);
+            }
+        }
+    }
+}
 
-    // dK (scaled) and dV rows of this wave's keys: register r holds key
-    // kw + row(r, hf), dims 2n and 2n + 1.
+// dQ_i = scale * sum_{j<=i} dS_ij K_j, one wave per (b, h, query block i),
+// query blocks from the last (most key blocks) to the first.
+__global__ __launch_bounds__(64) void bwd_dq_d64_kernel(float *__restrict__ grad_x,
+                                                        const float *__restrict__ dsw,
+                                                        const float *__restrict__ qkv,
+                                                        int T, int C, int H, int bh0, int BHc, int n_qb,
+                                                        float scale)
+{
+    const int lane = threadIdx.x, n = lane & 31, hf = lane >> 5;
+    const int i = n_qb - 1 - (int)(blockIdx.x / BHc);
+    const int bhl = (int)(blockIdx.x % BHc), bh = bh0 + bhl;
+    const int b = bh / H, h = bh % H;
+    const long W = 3L * C;
+    const float *kb = qkv + (long)b * T * W + C + (long)h * 64;
+    const float *ws = dsw + (long)bhl * ((long)n_qb * (n_qb + 1) / 2) * 1024;
+
+    // dQ[q][d] += dS[q][key] K[key][d]: step t of half hf contracts key
+    // 16 hf + t of the block. A operand dS[n][16 hf + t] (16 contiguous floats
+    // of the tile row), B operand K[key][2n, 2n + 1].
+    v16f a0 = zero16(), a1 = zero16();
+    for (int j = 0; j <= i; ++j)
+    {
+        const float4 *tile = reinterpret_cast<const float4 *>(ws + ds_tile(i, j) + n * 32 + 16 * hf);
+        float4 d4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            d4[u] = tile[u];
+        const float dsr[16] = {d4[0].x, d4[0].y, d4[0].z, d4[0].w, d4[1].x, d4[1].y, d4[1].z, d4[1].w,
+                               d4[2].x, d4[2].y, d4[2].z, d4[2].w, d4[3].x, d4[3].y, d4[3].z, d4[3].w};
+        const int kbase = 32 * j + 16 * hf;
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+        {
+            const float2 k2 = *reinterpret_cast<const float2 *>(kb + (long)min(kbase + t, T - 1) * W + 2 * n);
+            a0 = mfma32(dsr[t], k2.x, a0);
+            a1 = mfma32(dsr[t], k2.y, a1);
+        }
+    }
+    // register r of lane (n, hf): dQ[32 i + row(r, hf)][2n, 2n + 1]
 #pragma unroll
     for (int r = 0; r < 16; ++r)
     {
-        const int key = kw + mfma_row(r, hf);
-        if (key < T)
-        {
-            float *dst = gq + (long)key * W + 2 * n;
-            *reinterpret_cast<float2 *>(dst + C) = make_float2(dk0[r] * scale, dk1[r] * scale);
-            *reinterpret_cast<float2 *>(dst + 2 * C) = make_float2(dv0[r], dv1[r]);
-        }
+        const int row = 32 * i + mfma_row(r, hf);
+        if (row < T)
+            *reinterpret_cast<float2 *>(grad_x + ((long)b * T + row) * W + (long)h * 64 + 2 * n) =
+                make_float2(a0[r] * scale, a1[r] * scale);
     }
 }
 
@@ -412,8 +456,8 @@ __global__ __launch_bounds__(128) void bwd_dkdv_general_kernel(float *__restrict
 
 static float softmax_scale(int d) { return 1.0f / sqrtf((float)d); }
 
-static hipError_t launch_prep(float *grad_x, float *D, const float *dy, const float *y, const Shape &s,
-                              hipStream_t st, int zero_dq)
+hipError_t launch_bwd_prep(float *grad_x, float *D, const float *dy, const float *y, const Shape &s,
+                           hipStream_t st, int zero_dq)
 {
     const long items = (long)s.B * s.T * s.H;
     const int vec4 = (s.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(y) |
@@ -425,18 +469,44 @@ static hipError_t launch_prep(float *grad_x, float *D, const float *dy, const fl
     return hipGetLastError();
 }
 
-hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
-                          const float *qkv, const Shape &s, hipStream_t st)
+size_t bwd_d64_workspace_bytes(const Shape &s, int *bh_per_chunk)
 {
-    constexpr int QS = 2, BKV = 64 * QS;
-    hipError_t e = launch_prep(grad_x, D, dy, y, s, st, 1);
+    const long n_qb = (s.T + 31) / 32;
+    const size_t per_bh = (size_t)(n_qb * (n_qb + 1) / 2) * 4096;
+    const long BH = (long)s.B * s.H;
+    long chunk = (long)(kWorkspaceCap / per_bh);
+    chunk = chunk < 1 ? 1 : (chunk > BH ? BH : chunk);
+    if (bh_per_chunk)
+        *bh_per_chunk = (int)chunk;
+    return per_bh * (size_t)chunk;
+}
+
+hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
+                          const float *qkv, float *ws, int bh_per_chunk, const Shape &s, hipStream_t st)
+{
+    constexpr int NW = 4;
+    const long rows = (long)s.B * s.T;
+    hipLaunchKernelGGL(bwd_rowdot_d64_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, D, dy, y,
+                       rows, s.H);
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
-    const int n_kb = (s.T + BKV - 1) / BKV;
+    const int n_qb = (s.T + 31) / 32;
+    const int BH = s.B * s.H;
     const float scale = softmax_scale(64);
-    hipLaunchKernelGGL((bwd_d64_kernel<QS>), dim3((unsigned)((long)n_kb * s.B * s.H)), dim3(128 * QS), 0, st,
-                       grad_x, lse, D, dy, qkv, s.B, s.T, s.C, s.H, scale, scale * kLog2e);
-    return hipGetLastError();
+    for (int bh0 = 0; bh0 < BH; bh0 += bh_per_chunk)
+    {
+        const int cnt = BH - bh0 < bh_per_chunk ? BH - bh0 : bh_per_chunk;
+        const unsigned blocks = (unsigned)((long)n_qb * cnt);
+        hipLaunchKernelGGL((bwd_dkdv_d64_kernel<NW>), dim3(blocks), dim3(NW * 64), 0, st, grad_x, ws, lse, D, dy,
+                           qkv, s.T, s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale);
+        hipLaunchKernelGGL(bwd_dq_d64_kernel, dim3(blocks), dim3(64), 0, st, grad_x, ws, qkv, s.T, s.C, s.H, bh0,
+                           cnt, n_qb, scale);
+        e = hipGetLastError();
+        if (e != hipSuccess)
+            return e;
+    }
+    return hipSuccess;
 }
 
 template <int DM>
@@ -455,7 +525,7 @@ static void launch_bwd_general_dm(float *grad_x, const float *lse, const float *
 hipError_t launch_bwd_general(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
                               const float *qkv, const Shape &s, hipStream_t st)
 {
-    hipError_t e = launch_prep(grad_x, D, dy, y, s, st, 0);
+    hipError_t e = launch_bwd_prep(grad_x, D, dy, y, s, st, 0);
     if (e != hipSuccess)
         return e;
     if (s.d <= 16)

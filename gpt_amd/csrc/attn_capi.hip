@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -17,7 +18,10 @@
 namespace {
 
 thread_local char g_err[512] = "";
-int g_path = 0;  // 0 automatic, 1 general-d kernels only
+int g_path = 0;  // 0 automatic, 1 general-d kernels only, 2 atomic-dQ backward
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_pool_ready[kMaxDevices];
 
 int fail(int code, const char *fmt, ...)
 {
@@ -58,6 +62,32 @@ int check_device(const char *op)
     return 0;
 }
 
+// Stream-ordered dS workspace for the deterministic backward. The device's
+// default memory pool is told to keep freed memory (release threshold = max),
+// so after the first call hipMallocAsync / hipFreeAsync hand the same block
+// back without a device allocation; concurrent calls on different streams
+// each get their own block.
+hipError_t workspace_alloc(void **p, size_t bytes, hipStream_t st)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return e;
+    if (dev >= 0 && dev < kMaxDevices && g_pool_ready[dev].load(std::memory_order_acquire) == 0)
+    {
+        hipMemPool_t pool;
+        e = hipDeviceGetDefaultMemPool(&pool, dev);
+        if (e != hipSuccess)
+            return e;
+        uint64_t keep = UINT64_MAX;
+        e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+        if (e != hipSuccess)
+            return e;
+        g_pool_ready[dev].store(1, std::memory_order_release);
+    }
+    return hipMallocAsync(p, bytes, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -76,7 +106,7 @@ int gpt_hip_attn_fwd_f32(float *y, float *lse, const float *qkv, int batch_size,
     if (int rc = check_device(op))
         return rc;
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const bool mfma = g_path == 0 && s.d == 64 && aligned16(y) && aligned16(qkv);
+    const bool mfma = g_path != 1 && s.d == 64 && aligned16(y) && aligned16(qkv);
     const hipError_t e = mfma ? gpt_attn::launch_fwd_d64(y, lse, qkv, s, st)
                               : gpt_attn::launch_fwd_general(y, lse, qkv, s, st);
     if (e != hipSuccess)
@@ -99,12 +129,34 @@ int gpt_hip_attn_bwd_f32(float *grad_x, float *D_cache, const float *lse, const 
     if (int rc = check_device(op))
         return rc;
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const bool mfma = g_path == 0 && s.d == 64 && aligned16(grad_x) && aligned16(grad_y) && aligned16(y) &&
+    const bool mfma = g_path != 1 && s.d == 64 && aligned16(grad_x) && aligned16(grad_y) && aligned16(y) &&
                       aligned16(qkv);
-    const hipError_t e = mfma ? gpt_attn::launch_bwd_d64(grad_x, D_cache, lse, grad_y, y, qkv, s, st)
-                              : gpt_attn::launch_bwd_general(grad_x, D_cache, lse, grad_y, y, qkv, s, st);
+    if (!mfma)
+    {
+        const hipError_t e = gpt_attn::launch_bwd_general(grad_x, D_cache, lse, grad_y, y, qkv, s, st);
+        if (e != hipSuccess)
+            return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
+        return 0;
+    }
+    if (g_path == 2)
+    {
+        const hipError_t e = gpt_attn::launch_bwd_d64_atomic(grad_x, D_cache, lse, grad_y, y, qkv, s, st);
+        if (e != hipSuccess)
+            return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
+        return 0;
+    }
+    int chunk = 0;
+    const size_t bytes = gpt_attn::bwd_d64_workspace_bytes(s, &chunk);
+    void *ws = nullptr;
+    hipError_t e = workspace_alloc(&ws, bytes, st);
+    if (e != hipSuccess)
+        return fail(GPT_HIP_ATTN_ENOMEM, "%s: workspace of %zu bytes: %s", op, bytes, hipGetErrorString(e));
+    e = gpt_attn::launch_bwd_d64(grad_x, D_cache, lse, grad_y, y, qkv, static_cast<float *>(ws), chunk, s, st);
+    const hipError_t ef = hipFreeAsync(ws, st);
     if (e != hipSuccess)
         return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
+    if (ef != hipSuccess)
+        return fail(GPT_HIP_ATTN_ELAUNCH, "%s: workspace release failed: %s", op, hipGetErrorString(ef));
     return 0;
 }
 
@@ -118,7 +170,7 @@ int gpt_hip_attn_device_ok(void)
 
 int gpt_hip_attn_set_path(int path)
 {
-    if (path != 0 && path != 1)
+    if (path < 0 || path > 2)
         return fail(GPT_HIP_ATTN_EINVAL, "gpt_hip_attn_set_path: unknown path %d", path);
     const int prev = g_path;
     g_path = path;

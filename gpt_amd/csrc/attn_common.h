@@ -42,6 +42,38 @@ __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_lo
 // Value held by lane l ^ 32 (the other half of the wave64).
 __device__ __forceinline__ float swap_halves(float x) { return __shfl_xor(x, 32, 64); }
 
+// v_permlane32_swap with both operands = x: element 0 is x of lane l % 32
+// (the lower half's value), element 1 is x of lane 32 + l % 32 (the upper
+// half's value), in every lane. A VALU op, unlike the LDS bpermute that
+// __shfl_xor(x, 32) becomes.
+__device__ __forceinline__ float2 halves(float x)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// max / sum of x over lanes l and l ^ 32, the same bits in both lanes
+// (lower-half operand first).
+__device__ __forceinline__ float halves_max(float x)
+{
+    const float2 p = halves(x);
+    return fmaxf(p.x, p.y);
+}
+__device__ __forceinline__ float halves_sum(float x)
+{
+    const float2 p = halves(x);
+    return p.x + p.y;
+}
+
+// Compiler-level ordering point between one wave's LDS writes and its reads
+// of other lanes' values (a wave's LDS instructions execute in issue order).
+__device__ __forceinline__ void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ v16f zero16()
 {
     v16f z;

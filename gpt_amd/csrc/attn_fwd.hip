@@ -7,18 +7,29 @@
 // and replacing the reference's CUDA kernel (src/backend/cuda/kernels/
 // attention.cu:6-268).
 //
-// head_dim 64 kernel (fwd_d64_kernel): one wave owns 32 query rows; NW waves
-// of a workgroup share K/V tiles of BK keys staged in LDS. Both products run
-// on v_mfma_f32_32x32x2_f32 in the transposed orientation
+// head_dim 64 kernel (fwd_d64_kernel). Work unit = one 32-query block x one
+// 32-key block of the causal triangle. One workgroup per (b, h, query block);
+// its NW waves split the query block's key blocks (wave w takes blocks
+// w, w + NW, ...), each keeping its own online-softmax state, and merge the NW
+// partial (max, sum, O) triples through LDS at the end. Splitting the key
+// range keeps the longest wave at ceil(T / 32 / NW) units, so the causal
+// triangle's uneven rows balance across the chip even at T = 256.
+//
+// Both products run on v_mfma_f32_32x32x2_f32 in the transposed orientation
 //     S^T = K Q^T   (32 keys x 32 queries, 32 MFMAs over d = 64)
 //     O^T += V^T P^T (64 dims x 32 queries, 2 x 16 MFMAs over 32 keys)
 // so that each lane owns ONE query column: the row max / row sum of the online
-// softmax are 15 in-lane VALU ops plus one exchange with the other half-wave,
-// and the probabilities already sit where P^T's B operand needs them (the
-// key order of the PV contraction is permuted to the accumulator's row order,
-// so P never goes through LDS).
-// Q is held in registers pre-multiplied by log2(e)/sqrt(d), so the softmax
-// runs on v_exp_f32 (2^x) directly.
+// softmax are 15 in-lane VALU ops plus one v_permlane32_swap, and the
+// probabilities already sit where P^T's B operand needs them (the key order of
+// the PV contraction is permuted to the accumulator's row order, so P never
+// goes through LDS). K and V go from L2 straight into MFMA operand registers.
+// Q is held in registers pre-multiplied by log2(e)/sqrt(d), so the softmax runs
+// on v_exp_f32 (2^x) directly.
+//
+// Workgroup order: query blocks from the last (most key blocks) to the first,
+// (b, h) fastest. Workgroups go to the 8 XCDs round-robin, so when B*H is a
+// multiple of 8 every workgroup of one (b, h) lands on the same XCD and its
+// K/V stay in that XCD's L2.
 #include "attn_common.h"
 #include "attn_kernels.h"
 
@@ -26,158 +37,163 @@
 
 namespace gpt_attn {
 
-// float4 number `idx` of a 64-wide K/V tile starting at key k0 (16 per row).
-// Rows at or beyond T are read from row T-1 (always mapped) and replaced by
-// zeros with a select, which keeps the load unconditional.
-__device__ __forceinline__ void load_kv_f4(float4 &k, float4 &v, const float *base, int idx, int k0, int T,
-                                           int C, long W)
-{
-    const int key = k0 + (idx >> 4), c4 = (idx & 15) * 4;
-    const float *src = base + (long)min(key, T - 1) * W + c4;
-    const float4 kk = *reinterpret_cast<const float4 *>(src + C);
-    const float4 vv = *reinterpret_cast<const float4 *>(src + 2 * C);
-    const bool ok = key < T;
-    k = make_float4(ok ? kk.x : 0.f, ok ? kk.y : 0.f, ok ? kk.z : 0.f, ok ? kk.w : 0.f);
-    v = make_float4(ok ? vv.x : 0.f, ok ? vv.y : 0.f, ok ? vv.z : 0.f, ok ? vv.w : 0.f);
-}
-
-template <int NW, int BK>
+template <int NW>
 __global__ __launch_bounds__(NW * 64) void fwd_d64_kernel(float *__restrict__ y,
                                                           float *__restrict__ lse,
                                                           const float *__restrict__ qkv,
-                                                          int B, int T, int C, int H,
-                                                          float qscale, int n_qt)
+                                                          int T, int C, int H, int BH, int n_qb,
+                                                          float qscale)
 {
-    constexpr int D = 64, ST = kRowStride, NT = NW * 64;
-    constexpr int LOADS = BK * 16 / NT;  // float4 of one K (or V) tile per thread
-    static_assert((BK * 16) % NT == 0 && BK % 32 == 0, "tile shape");
-    __shared__ __attribute__((aligned(16))) float ks[BK * ST];
-    __shared__ __attribute__((aligned(16))) float vs[BK * ST];
-
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int n = lane & 31, hf = lane >> 5;
-    const int BH = B * H;
-    // Heaviest query tiles (most key tiles under the causal mask) go first.
-    const int qt = n_qt - 1 - (int)(blockIdx.x / BH);
-    const int bh = blockIdx.x % BH;
+    const int qb = n_qb - 1 - (int)(blockIdx.x / BH);
+    const int bh = (int)(blockIdx.x % BH);
     const int b = bh / H, h = bh % H;
     const long W = 3L * C;
-    const float *base = qkv + (long)b * T * W + (long)h * D;
-    const int q0 = qt * 32 * NW;
-    const int qw = q0 + 32 * w;  // first query row of this wave
+    const float *base = qkv + (long)b * T * W + (long)h * 64;
+    const int q0 = 32 * qb;
 
-    // B operand of S^T = K Q^T: lane (n, hf) holds Q[qw+n][32*hf + s], s = 0..31.
-    // Rows at or beyond T read as zeros.
+    // B operand of S^T = K Q^T: lane (n, hf) holds Q[q0 + n][32 hf + s].
+    // Rows at or beyond T are read from row T - 1; their outputs are dropped.
     float qreg[32];
     {
-        const int row = qw + n;
-        const float4 *src =
-            reinterpret_cast<const float4 *>(base + (long)min(row, T - 1) * W + 32 * hf);
+        const float4 *src = reinterpret_cast<const float4 *>(base + (long)min(q0 + n, T - 1) * W + 32 * hf);
 #pragma unroll
         for (int t = 0; t < 8; ++t)
         {
             const float4 v = src[t];
-            qreg[4 * t + 0] = row < T ? v.x * qscale : 0.f;
-            qreg[4 * t + 1] = row < T ? v.y * qscale : 0.f;
-            qreg[4 * t + 2] = row < T ? v.z * qscale : 0.f;
-            qreg[4 * t + 3] = row < T ? v.w * qscale : 0.f;
+            qreg[4 * t + 0] = v.x * qscale;
+            qreg[4 * t + 1] = v.y * qscale;
+            qreg[4 * t + 2] = v.z * qscale;
+            qreg[4 * t + 3] = v.w * qscale;
         }
     }
 
-    v16f o0 = zero16(), o1 = zero16();  // O^T rows d = 2*row + 0 / + 1
+    v16f o0 = zero16(), o1 = zero16();  // O^T rows d = 2 * row + 0 / + 1
     float m = -INFINITY, l = 0.f;       // running max (log2 units) and sum
 
-    const int kend = min(T, q0 + 32 * NW);  // keys [0, kend) are visible to the tile
-    const int ntiles = (kend + BK - 1) / BK;
-
-    // Next tile's K/V, loaded into registers while the current tile is used.
-    float4 kpre[LOADS], vpre[LOADS];
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i)
-        load_kv_f4(kpre[i], vpre[i], base, tid + i * NT, 0, T, C, W);
-    for (int kt = 0; kt < ntiles; ++kt)
+    for (int j = w; j <= qb; j += NW)
     {
-        __syncthreads();  // every wave is done reading the previous tile
-#pragma unroll
-        for (int i = 0; i < LOADS; ++i)
+        const int k0 = 32 * j;
+        // A operand of S^T: lane (n, hf) holds K[k0 + n][32 hf + s].
+        float4 kv[8];
         {
-            const int idx = tid + i * NT, r = idx >> 4, c4 = (idx & 15) * 4;
-            *reinterpret_cast<float4 *>(&ks[r * ST + c4]) = kpre[i];
-            *reinterpret_cast<float4 *>(&vs[r * ST + c4]) = vpre[i];
-        }
-        __syncthreads();
-        if (kt + 1 < ntiles)
-        {
-#pragma unroll
-            for (int i = 0; i < LOADS; ++i)
-                load_kv_f4(kpre[i], vpre[i], base, tid + i * NT, (kt + 1) * BK, T, C, W);
-        }
-
-#pragma unroll
-        for (int sub = 0; sub < BK / 32; ++sub)
-        {
-            const int kk0 = kt * BK + 32 * sub;
-            if (kk0 > qw + 31)
-                continue;  // keys all above this wave's queries (wave-uniform)
-
-            // S^T[key kk0 + row(r)][query qw + n], in log2 units.
-            v16f s = zero16();
-            const float *krow = &ks[(32 * sub + n) * ST + 32 * hf];
+            const float4 *src =
+                reinterpret_cast<const float4 *>(base + (long)min(k0 + n, T - 1) * W + C + 32 * hf);
 #pragma unroll
             for (int t = 0; t < 8; ++t)
-            {
-                const float4 kv = *reinterpret_cast<const float4 *>(krow + 4 * t);
-                s = mfma32(kv.x, qreg[4 * t + 0], s);
-                s = mfma32(kv.y, qreg[4 * t + 1], s);
-                s = mfma32(kv.z, qreg[4 * t + 2], s);
-                s = mfma32(kv.w, qreg[4 * t + 3], s);
-            }
-            if (kk0 + 31 > qw)
-            {
-                // diagonal tile: key kk0 + row > query qw + n is masked out
+                kv[t] = src[t];
+        }
+        // A operand of O^T += V^T P^T, step st: V[k0 + row(st, hf)][2n, 2n + 1].
+        float2 vv[16];
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (kk0 + mfma_row(r, hf) > qw + n)
-                        s[r] = -INFINITY;
-            }
-            float mt = s[0];
+        for (int st = 0; st < 16; ++st)
+            vv[st] = *reinterpret_cast<const float2 *>(base + (long)min(k0 + mfma_row(st, hf), T - 1) * W +
+                                                      2 * C + 2 * n);
+
+        // S^T[key k0 + row(r)][query q0 + n], in log2 units.
+        v16f s = zero16();
 #pragma unroll
-            for (int r = 1; r < 16; ++r)
-                mt = fmaxf(mt, s[r]);
-            mt = fmaxf(mt, swap_halves(mt));
-            const float mn = fmaxf(m, mt);
-            const float corr = fast_exp2(m - mn);
-            float ps = 0.f;
+        for (int t = 0; t < 8; ++t)
+        {
+            s = mfma32(kv[t].x, qreg[4 * t + 0], s);
+            s = mfma32(kv[t].y, qreg[4 * t + 1], s);
+            s = mfma32(kv[t].z, qreg[4 * t + 2], s);
+            s = mfma32(kv[t].w, qreg[4 * t + 3], s);
+        }
+        if (j == qb)
+        {
+            // diagonal block: key k0 + row > query q0 + n is masked out (this
+            // also masks keys at or beyond T for every valid query)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (mfma_row(r, hf) > n)
+                    s[r] = -INFINITY;
+        }
+        float mt = s[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r)
+            mt = fmaxf(mt, s[r]);
+        mt = halves_max(mt);
+        const float mn = fmaxf(m, mt);
+        const float corr = fast_exp2(m - mn);
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+        {
+            s[r] = fast_exp2(s[r] - mn);
+            ps += s[r];
+        }
+        l = l * corr + halves_sum(ps);
+        m = mn;
+        o0 *= corr;
+        o1 *= corr;
+
+        // O^T += V^T P^T: step st contracts key k0 + row(st, hf) for this
+        // half, which is exactly the key of accumulator register st.
+#pragma unroll
+        for (int st = 0; st < 16; ++st)
+        {
+            o0 = mfma32(vv[st].x, s[st], o0);
+            o1 = mfma32(vv[st].y, s[st], o1);
+        }
+    }
+
+    if constexpr (NW > 1)
+    {
+        // Merge the waves' partial states; wave 0 finishes. Layout
+        // [wave][register][lane] keeps every LDS access lane-contiguous.
+        __shared__ float sm_m[NW][32], sm_l[NW][32];
+        __shared__ float sm_o[NW - 1][32][64];
+        if (w > 0)
+        {
 #pragma unroll
             for (int r = 0; r < 16; ++r)
             {
-                s[r] = fast_exp2(s[r] - mn);
-                ps += s[r];
-            }
-            ps += swap_halves(ps);
-            l = l * corr + ps;
-            m = mn;
-            o0 *= corr;
-            o1 *= corr;
-
-            // O^T += V^T P^T: step st contracts key kk0 + row(st, hf) for this
-            // half, which is exactly the key of accumulator register st.
-#pragma unroll
-            for (int st = 0; st < 16; ++st)
-            {
-                const float2 vv =
-                    *reinterpret_cast<const float2 *>(&vs[(32 * sub + mfma_row(st, hf)) * ST + 2 * n]);
-                o0 = mfma32(vv.x, s[st], o0);
-                o1 = mfma32(vv.y, s[st], o1);
+                sm_o[w - 1][r][lane] = o0[r];
+                sm_o[w - 1][16 + r][lane] = o1[r];
             }
         }
+        if (hf == 0)
+        {
+            sm_m[w][n] = m;
+            sm_l[w][n] = l;
+        }
+        __syncthreads();
+        if (w > 0)
+            return;
+        float mw[NW], M = m;
+#pragma unroll
+        for (int v = 0; v < NW; ++v)
+        {
+            mw[v] = sm_m[v][n];
+            M = fmaxf(M, mw[v]);
+        }
+        // wave 0 always holds key block 0, so M is finite
+        const float f0 = fast_exp2(m - M);
+        l *= f0;
+        o0 *= f0;
+        o1 *= f0;
+#pragma unroll
+        for (int v = 1; v < NW; ++v)
+        {
+            const float f = fast_exp2(mw[v] - M);  // 0 for a wave that saw no key block
+            l += f * sm_l[v][n];
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+            {
+                o0[r] += f * sm_o[v - 1][r][lane];
+                o1[r] += f * sm_o[v - 1][16 + r][lane];
+            }
+        }
+        m = M;
     }
 
-    const int row = qw + n;
+    const int row = q0 + n;
     if (row < T)
     {
         const float inv = 1.f / l;
-        float *dst = y + ((long)b * T + row) * C + (long)h * D;
+        float *dst = y + ((long)b * T + row) * C + (long)h * 64;
 #pragma unroll
         for (int g = 0; g < 4; ++g)
         {
@@ -194,8 +210,8 @@ __global__ __launch_bounds__(NW * 64) void fwd_d64_kernel(float *__restrict__ y,
     }
 }
 
-// General head_dim (1..DM): one thread per (b, h, query row), two-pass-free
-// online softmax over keys 0..i, q and the output row in registers.
+// General head_dim (1..DM): one thread per (b, h, query row), online softmax
+// over keys 0..i, q and the output row in registers.
 template <int DM>
 __global__ __launch_bounds__(128) void fwd_general_kernel(float *__restrict__ y,
                                                           float *__restrict__ lse,
@@ -252,12 +268,13 @@ static float softmax_scale(int d) { return 1.0f / sqrtf((float)d); }
 
 hipError_t launch_fwd_d64(float *y, float *lse, const float *qkv, const Shape &s, hipStream_t st)
 {
-    constexpr int NW = 4, BK = 64;
-    const int n_qt = (s.T + 32 * NW - 1) / (32 * NW);
-    const long blocks = (long)n_qt * s.B * s.H;
+    constexpr int NW = 4;
+    const int n_qb = (s.T + 31) / 32;
+    const int BH = s.B * s.H;
+    const long blocks = (long)n_qb * BH;
     const float qscale = softmax_scale(64) * kLog2e;
-    hipLaunchKernelGGL((fwd_d64_kernel<NW, BK>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, y, lse,
-                       qkv, s.B, s.T, s.C, s.H, qscale, n_qt);
+    hipLaunchKernelGGL((fwd_d64_kernel<NW>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, y, lse, qkv, s.T,
+                       s.C, s.H, BH, n_qb, qscale);
     return hipGetLastError();
 }
 

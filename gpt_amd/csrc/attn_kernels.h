@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 
 namespace gpt_attn {
 
@@ -11,19 +12,36 @@ struct Shape
     int B, T, C, H, d;
 };
 
+// Largest dS workspace one backward call asks for; bigger problems are
+// processed in chunks of (b, h) pairs that fit.
+constexpr size_t kWorkspaceCap = size_t(2) << 30;
+
 // Forward, head_dim 64, fp32 MFMA. Pointers 16-byte aligned.
 hipError_t launch_fwd_d64(float *y, float *lse, const float *qkv, const Shape &s, hipStream_t st);
 
 // Forward, any head_dim in 1..256, scalar HIP kernel.
 hipError_t launch_fwd_general(float *y, float *lse, const float *qkv, const Shape &s, hipStream_t st);
 
-// Backward, head_dim 64, fp32 MFMA (D rows + dQ zeroing, then the fused
-// dK/dV/dQ kernel with atomic dQ accumulation).
-hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float *dy,
-                          const float *y, const float *qkv, const Shape &s, hipStream_t st);
+// D = rowsum(dO * O) for any head_dim; optionally zeroes the dQ third of grad_x.
+hipError_t launch_bwd_prep(float *grad_x, float *D, const float *dy, const float *y, const Shape &s,
+                           hipStream_t st, int zero_dq);
+
+// Bytes of dS workspace launch_bwd_d64 needs, and the number of (b, h) pairs
+// processed per chunk with it.
+size_t bwd_d64_workspace_bytes(const Shape &s, int *bh_per_chunk);
+
+// Backward, head_dim 64, fp32 MFMA, deterministic (D rows, dK/dV + dS tiles,
+// dQ from the dS tiles). `ws` holds bwd_d64_workspace_bytes(s) bytes.
+hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
+                          const float *qkv, float *ws, int bh_per_chunk, const Shape &s, hipStream_t st);
+
+// Backward, head_dim 64, fp32 MFMA with fp32-atomic dQ accumulation (D rows +
+// dQ zeroing, then the fused dK/dV/dQ kernel).
+hipError_t launch_bwd_d64_atomic(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
+                                 const float *qkv, const Shape &s, hipStream_t st);
 
 // Backward, any head_dim in 1..256, scalar HIP kernels (no atomics).
-hipError_t launch_bwd_general(float *grad_x, float *D, const float *lse, const float *dy,
-                              const float *y, const float *qkv, const Shape &s, hipStream_t st);
+hipError_t launch_bwd_general(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
+                              const float *qkv, const Shape &s, hipStream_t st);
 
 }  // namespace gpt_attn

@@ -18,7 +18,12 @@
  *       D_cache [B, T, H]
  *   - Softmax scale is 1/sqrt(d); the causal mask keeps key j <= query i.
  *   - `stream` is a hipStream_t passed as void*; NULL means the default stream.
- *     Work is enqueued asynchronously; nothing is allocated on the device.
+ *     Work is enqueued asynchronously. The forward allocates nothing. The
+ *     head_dim-64 backward takes a stream-ordered dS workspace from the
+ *     device's default memory pool (hipMallocAsync / hipFreeAsync on
+ *     `stream`; 4 KiB per 32x32 causal tile, 28 MiB at B=16 T=256 H=12, at
+ *     most 2 GiB per call: larger problems run in (b, h) chunks); the pool is
+ *     set to keep freed memory, so steady-state calls do not allocate.
  *   - Return 0 on success or a negative GPT_HIP_ATTN_E* code; the message of
  *     the last failure on the calling thread is kept for
  *     gpt_hip_attn_last_error(). Inputs are never modified.
@@ -26,7 +31,8 @@
  *   - head_dim 64 runs the fp32-MFMA kernels (pointers must be 16-byte
  *     aligned, which the reference's 4-float tensor padding guarantees);
  *     any other head_dim in 1..256, or a misaligned pointer, runs the
- *     general-d HIP kernels.
+ *     general-d HIP kernels. Results are bitwise reproducible run to run
+ *     (no atomics) unless path 2 is selected.
  */
 #ifndef GPT_HIP_ATTN_H
 #define GPT_HIP_ATTN_H
@@ -44,6 +50,7 @@ extern "C" {
 #define GPT_HIP_ATTN_ENODEV (-4)     /* no usable HIP device */
 #define GPT_HIP_ATTN_ELAUNCH (-5)    /* a kernel launch failed */
 #define GPT_HIP_ATTN_ERANGE (-6)     /* tensor too large for the index types */
+#define GPT_HIP_ATTN_ENOMEM (-7)     /* the backward's workspace could not be allocated */
 
 /* Causal attention forward: writes every element of y and lse.
  * Replaces IGPTBackend::device_flash_attention_forward
@@ -80,6 +87,9 @@ int gpt_hip_attn_device_ok(void);
  *           kernels otherwise
  *   path 1  always the general-d kernels (a second, independent HIP
  *           implementation used to cross-check the MFMA kernels)
+ *   path 2  as 0, but the head_dim-64 backward accumulates dQ with fp32
+ *           global atomics (no workspace, not bitwise reproducible); kept to
+ *           measure that design against the default
  * Returns the previous path, or GPT_HIP_ATTN_EINVAL for an unknown path.
  * No reference counterpart. */
 int gpt_hip_attn_set_path(int path);

@@ -118,6 +118,19 @@ def test_general_head_dim(dev, B, T, C, H):
     check_fwd_bwd(dev, x, g, H, tag=f"d={C // H}")
 
 
+@pytest.mark.parametrize("B,T", [(8, 256), (2, 97), (1, 33)])
+def test_atomic_dq_path_parity(dev, B, T):
+    """The fp32-atomic dQ backward (path 2) against the oracle."""
+    C, H = 768, 12
+    x = synth.qkv(B, T, C, seed=77 + T)
+    g = synth.grad_out(B, T, C, seed=77 + T)
+    prev = gpt_amd.set_path(2)
+    try:
+        check_fwd_bwd(dev, x, g, H, tag=f"atomic T={T}")
+    finally:
+        gpt_amd.set_path(prev)
+
+
 def test_general_path_agrees_with_mfma_path(dev):
     B, T, C, H = 2, 200, 256, 4
     x = synth.qkv(B, T, C, seed=11)
@@ -202,10 +215,20 @@ def test_backward_overwrites_grad_x_and_is_repeatable(dev):
     gpt_amd.device_flash_attention_backward(gx, D, lse, g, y, x, B, T, C, H)
     torch.cuda.synchronize()
     assert torch.isfinite(first).all()
-    # dK, dV are written with plain stores: bit-identical run to run;
-    # dQ is accumulated with atomics: equal within tolerance
-    assert torch.equal(first[..., C:], gx[..., C:])
-    assert rel_err(first[..., :C].cpu().numpy(), gx[..., :C].cpu().numpy()) <= 1e-6
+    # no atomics on the default path: bit-identical run to run
+    assert torch.equal(first, gx)
+    # the atomic-dQ path (another kernel, other summation orders) overwrites
+    # grad_x too and agrees within fp32 rounding
+    prev = gpt_amd.set_path(2)
+    try:
+        gx.fill_(float("nan"))
+        gpt_amd.device_flash_attention_backward(gx, D, lse, g, y, x, B, T, C, H)
+        torch.cuda.synchronize()
+    finally:
+        gpt_amd.set_path(prev)
+    assert torch.isfinite(gx).all()
+    for sl in (slice(0, C), slice(C, 2 * C), slice(2 * C, 3 * C)):
+        assert rel_err(gx[..., sl].cpu().numpy(), first[..., sl].cpu().numpy()) <= 1e-6
 
 
 def test_inputs_untouched_and_side_stream(dev):
