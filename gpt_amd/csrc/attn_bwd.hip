@@ -122,220 +122,362 @@ __global__ __launch_bounds__(256) void bwd_rowdot_d64_kernel(float *__restrict__
 // Offset (floats) of dS tile (i, j), j <= i, inside one (b, h)'s workspace.
 __device__ __forceinline__ long ds_tile(int i, int j) { return ((long)i * (i + 1) / 2 + j) * 1024; }
 
-template <int NW>
-__global__ __launch_bounds__(NW * 64) void bwd_dkdv_d64_kernel(float *__restrict__ grad_x,
-                                                               float *__restrict__ dsw,
-                                                               const float *__restrict__ lse,
-                                                               const float *__restrict__ Dv,
-                                                               const float *__restrict__ dy,
-                                                               const float *__restrict__ qkv,
-                                                               int T, int C, int H, int bh0, int BHc,
-                                                               int n_qb, float c2, float scale)
+// Sum one 64-register-per-lane partial (v0..v3, 16 registers each) over the
+// NW = 4 waves of the workgroup in the fixed order (w0 + w1) + (w2 + w3);
+// wave 0 ends with the total. `red` holds two [64][64] partials.
+__device__ __forceinline__ void reduce4(v16f &v0, v16f &v1, v16f &v2, v16f &v3, float (*red)[64][64], int w,
+                                        int lane)
 {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (w & 1)
+    {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+        {
+            red[w >> 1][r][lane] = v0[r];
+            red[w >> 1][16 + r][lane] = v1[r];
+            red[w >> 1][32 + r][lane] = v2[r];
+            red[w >> 1][48 + r][lane] = v3[r];
+        }
+    }
+    __syncthreads();
+    if (!(w & 1))
+    {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+        {
+            v0[r] += red[w >> 1][r][lane];
+            v1[r] += red[w >> 1][16 + r][lane];
+            v2[r] += red[w >> 1][32 + r][lane];
+            v3[r] += red[w >> 1][48 + r][lane];
+        }
+    }
+    __syncthreads();
+    if (w == 2)
+    {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+        {
+            red[0][r][lane] = v0[r];
+            red[0][16 + r][lane] = v1[r];
+            red[0][32 + r][lane] = v2[r];
+            red[0][48 + r][lane] = v3[r];
+        }
+    }
+    __syncthreads();
+    if (w == 0)
+    {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+        {
+            v0[r] += red[0][r][lane];
+            v1[r] += red[0][16 + r][lane];
+            v2[r] += red[0][32 + r][lane];
+            v3[r] += red[0][48 + r][lane];
+        }
+    }
+}
+
+// dK, dV and the dS tiles. One workgroup per (b, h, key-block pair
+// (p, n - 1 - p)): key block j has n - j units (query blocks j .. n - 1), so
+// each pair carries n + 1 units. The pair's two key blocks are done one after
+// the other; for each, K and V are staged once in LDS (row stride
+// kRowStride) and the 4 waves split its query blocks round-robin (rotated per
+// workgroup), accumulating partial dK / dV in registers that are summed
+// through LDS in a fixed order and stored by wave 0.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void bwd_dkdv_d64_kernel(
+    float *__restrict__ grad_x, float *__restrict__ dsw, const float *__restrict__ lse,
+    const float *__restrict__ Dv, const float *__restrict__ dy, const float *__restrict__ qkv, int T, int C, int H,
+    int bh0, int BHc, int n_qb, float c2, float scale)
+{
+    constexpr int NW = 4, ST = kRowStride;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int n = lane & 31, hf = lane >> 5;
-    // key block j, lowest first (it has the most query blocks)
-    const int j = (int)(blockIdx.x / BHc);
+    const int pr = (int)(blockIdx.x / BHc);
     const int bhl = (int)(blockIdx.x % BHc), bh = bh0 + bhl;
     const int b = bh / H, h = bh % H;
-    const long W = 3L * C;
-    const float *qb_ = qkv + (long)b * T * W + (long)h * 64;
-    const float *dob = dy + (long)b * T * C + (long)h * 64;
-    const float *lb = lse + (long)b * T * H + h;
-    const float *db = Dv + (long)b * T * H + h;
+    const uint32_t Wb = 12u * (uint32_t)C, Cb = 4u * (uint32_t)C, Hb = 4u * (uint32_t)H;
+    const rsrc_t rq = make_rsrc(qkv + (long)b * T * 3L * C + (long)h * 64,
+                                (uint32_t)(((long)T * 3 * C - (long)h * 64) * 4));
+    const rsrc_t ro = make_rsrc(dy + (long)b * T * C + (long)h * 64, (uint32_t)(((long)T * C - (long)h * 64) * 4));
+    const rsrc_t rl = make_rsrc(lse + (long)b * T * H + h, (uint32_t)(((long)T * H - h) * 4));
+    const rsrc_t rd = make_rsrc(Dv + (long)b * T * H + h, (uint32_t)(((long)T * H - h) * 4));
     float *ws = dsw + (long)bhl * ((long)n_qb * (n_qb + 1) / 2) * 1024;
-    const int k0 = 32 * j;
+    float *gx = grad_x + (long)b * T * 3L * C + (long)h * 64;
 
-    // B operands of S = Q K^T and dP = dO V^T: lane (n, hf) holds
-    // K[k0 + n][32 hf + s] and V[k0 + n][32 hf + s]. Keys at or beyond T are
-    // read from row T - 1; they only meet masked (query < key) entries.
-    float4 kop[8], vop[8];
+    __shared__ __attribute__((aligned(16))) float kv_lds[2][32 * ST];  // K, V of the key block
+    __shared__ __attribute__((aligned(16))) float ld_lds[NW][2][32];   // per wave: L * log2(e), D
+    __shared__ float red[2][64][64];
+
+    for (int it = 0; it < 2; ++it)
     {
-        const float *src = qb_ + (long)min(k0 + n, T - 1) * W + 32 * hf;
+        const int j = it == 0 ? pr : n_qb - 1 - pr;
+        if (it == 1 && j == pr)
+            break;  // odd n_qb: the middle key block has no partner
+        const int k0 = 32 * j;
+        __syncthreads();  // the previous key block's LDS reads are done
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
+        for (int u = 0; u < 4; ++u)
         {
-            kop[t] = reinterpret_cast<const float4 *>(src + C)[t];
-            vop[t] = reinterpret_cast<const float4 *>(src + 2 * C)[t];
-        }
-    }
-
-    __shared__ __attribute__((aligned(16))) float sm_ld[NW][2][32];  // per wave: L * log2(e), D
-    v16f dk0 = zero16(), dk1 = zero16(), dv0 = zero16(), dv1 = zero16();
-
-    for (int i = j + w; i < n_qb; i += NW)
-    {
-        const int q0 = 32 * i;
-        const int qr = min(q0 + n, T - 1);
-        if (hf == 0)
-        {
-            sm_ld[w][0][n] = lb[(long)qr * H] * kLog2e;
-            sm_ld[w][1][n] = db[(long)qr * H];
-        }
-        // S[query q0 + row(r)][key k0 + n] and dP likewise; A operands
-        // Q[q0 + n][32 hf + s] and dO[q0 + n][32 hf + s].
-        v16f s = zero16(), dp = zero16();
-        {
-            const float4 *qs = reinterpret_cast<const float4 *>(qb_ + (long)qr * W + 32 * hf);
-            const float4 *os = reinterpret_cast<const float4 *>(dob + (long)qr * C + 32 * hf);
-#pragma unroll
-            for (int t = 0; t < 8; ++t)
-            {
-                const float4 qa = qs[t], oa = os[t];
-                s = mfma32(qa.x, kop[t].x, s);
-                dp = mfma32(oa.x, vop[t].x, dp);
-                s = mfma32(qa.y, kop[t].y, s);
-                dp = mfma32(oa.y, vop[t].y, dp);
-                s = mfma32(qa.z, kop[t].z, s);
-                dp = mfma32(oa.z, vop[t].z, dp);
-                s = mfma32(qa.w, kop[t].w, s);
-                dp = mfma32(oa.w, vop[t].w, dp);
-            }
-        }
-        wave_lds_sync();
-        // P and dS (without the 1/sqrt(d)); zero where key > query or the
-        // query row is past T.
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-        {
-            const float4 l4 = *reinterpret_cast<const float4 *>(&sm_ld[w][0][8 * g + 4 * hf]);
-            const float4 d4 = *reinterpret_cast<const float4 *>(&sm_ld[w][1][8 * g + 4 * hf]);
-            const float lj[4] = {l4.x, l4.y, l4.z, l4.w};
-            const float dj[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
-            {
-                const int r = 4 * g + jj;
-                const int qrow = q0 + 8 * g + 4 * hf + jj;  // = q0 + row(r, hf)
-                const bool keep = (k0 + n <= qrow) && (qrow < T);
-                const float p = fast_exp2(s[r] * c2 - lj[jj]);
-                s[r] = keep ? p : 0.f;
-                dp[r] = keep ? p * (dp[r] - dj[jj]) : 0.f;
-            }
-        }
-        // dS tile, query-major (row = query, column = key).
-        {
-            float *tile = ws + ds_tile(i, j);
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                tile[mfma_row(r, hf) * 32 + n] = dp[r];
-        }
-        // dV += P^T dO and dK += dS^T Q; step st contracts query
-        // q0 + row(st, hf), the query of accumulator register st. B operands
-        // dO / Q[q0 + row(st, hf)][2n, 2n + 1].
-#pragma unroll
-        for (int st = 0; st < 16; ++st)
-        {
-            const long rr = min(q0 + mfma_row(st, hf), T - 1);
-            const float2 g2 = *reinterpret_cast<const float2 *>(dob + rr * C + 2 * n);
-            const float2 q2 = *reinterpret_cast<const float2 *>(qb_ + rr * W + 2 * n);
-            dv0 = mfma32(s[st], g2.x, dv0);
-            dv1 = mfma32(s[st], g2.y, dv1);
-            dk0 = mfma32(dp[st], q2.x, dk0);
-            dk1 = mfma32(dp[st], q2.y, dk1);
-        }
-        wave_lds_sync();
-    }
-
-    // Sum the NW partial dK / dV in wave order and store. Register r of lane
-    // (n, hf) holds key k0 + row(r, hf), dims 2n (dk0, dv0) and 2n + 1.
-    constexpr int RPW = 16 / NW;  // registers finished by each wave
-    if constexpr (NW > 1)
-    {
-        __shared__ float sm_red[NW][64][64];  // [wave][value][lane]
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-        {
-            sm_red[w][r][lane] = dk0[r];
-            sm_red[w][16 + r][lane] = dk1[r];
-            sm_red[w][32 + r][lane] = dv0[r];
-            sm_red[w][48 + r][lane] = dv1[r];
+            const int idx = tid + 256 * u, which = idx >> 9, r = (idx >> 4) & 31, c4 = idx & 15;
+            const float4 v = bload4(rq, (uint32_t)(k0 + r) * Wb + (1u + which) * Cb + 16u * c4);
+            *reinterpret_cast<float4 *>(&kv_lds[which][r * ST + 4 * c4]) = v;
         }
         __syncthreads();
-#pragma unroll
-        for (int u = 0; u < RPW; ++u)
+
+        // wave w takes query blocks i = j + u with (u + rot) % NW == w
+        const int rot = (pr + (it == 0 ? 0 : n_qb - pr)) % NW;
+        const int u0 = (w - rot + NW) % NW;
+        v16f dk0 = zero16(), dk1 = zero16(), dv0 = zero16(), dv1 = zero16();
+        for (int i = j + u0; i < n_qb; i += NW)
         {
-            const int r = w * RPW + u;
-            float a0 = 0.f, a1 = 0.f, c0 = 0.f, c1 = 0.f;
+            const int q0 = 32 * i;
+            if (hf == 0)
+            {
+                ld_lds[w][0][n] = bload1(rl, (uint32_t)(q0 + n) * Hb) * kLog2e;
+                ld_lds[w][1][n] = bload1(rd, (uint32_t)(q0 + n) * Hb);
+            }
+            // S[query q0 + row(r)][key k0 + n] and dP likewise. A operands
+            // Q / dO[q0 + n][32 hf + s] (global), B operands K / V[k0 + n][32 hf + s]
+            // (LDS).
+            // Four chunks of two float4 each; chunk c + 1's loads are issued
+            // before chunk c's MFMAs (two register buffers in flight).
+            v16f s = zero16(), dp = zero16();
+            {
+                const uint32_t qo = (uint32_t)(q0 + n) * Wb + 128u * hf;
+                const uint32_t oo = (uint32_t)(q0 + n) * Cb + 128u * hf;
+                const float *kr = &kv_lds[0][n * ST + 32 * hf];
+                const float *vr = &kv_lds[1][n * ST + 32 * hf];
+                float4 qa[2][2], oa[2][2];
 #pragma unroll
-            for (int v = 0; v < NW; ++v)
-            {
-                a0 += sm_red[v][r][lane];
-                a1 += sm_red[v][16 + r][lane];
-                c0 += sm_red[v][32 + r][lane];
-                c1 += sm_red[v][48 + r][lane];
+                for (int e = 0; e < 2; ++e)
+                {
+                    qa[0][e] = bload4(rq, qo + 16u * e);
+                    oa[0][e] = bload4(ro, oo + 16u * e);
+                }
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                {
+                    if (c < 3)
+                    {
+#pragma unroll
+                        for (int e = 0; e < 2; ++e)
+                        {
+                            qa[(c + 1) & 1][e] = bload4(rq, qo + 16u * (2 * c + 2 + e));
+                            oa[(c + 1) & 1][e] = bload4(ro, oo + 16u * (2 * c + 2 + e));
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int e = 0; e < 2; ++e)
+                    {
+                        const int t = 2 * c + e;
+                        const float4 q4 = qa[c & 1][e], o4 = oa[c & 1][e];
+                        const float4 kb = *reinterpret_cast<const float4 *>(kr + 4 * t);
+                        const float4 vb = *reinterpret_cast<const float4 *>(vr + 4 * t);
+                        s = mfma32(q4.x, kb.x, s);
+                        dp = mfma32(o4.x, vb.x, dp);
+                        s = mfma32(q4.y, kb.y, s);
+                        dp = mfma32(o4.y, vb.y, dp);
+                        s = mfma32(q4.z, kb.z, s);
+                        dp = mfma32(o4.z, vb.z, dp);
+                        s = mfma32(q4.w, kb.w, s);
+                        dp = mfma32(o4.w, vb.w, dp);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
-            const int key = k0 + mfma_row(r, hf);
-            if (key < T)
+            wave_lds_sync();
+            // Phase boundaries keep the scheduler from hoisting the next
+            // phase's loads into this one (register pressure -> occupancy).
+            __builtin_amdgcn_sched_barrier(0);
+            // P and dS (without the 1/sqrt(d)); zero where key > query or the
+            // query row is past T.
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
             {
-                float *dst = grad_x + ((long)b * T + key) * W + (long)h * 64 + 2 * n;
-                *reinterpret_cast<float2 *>(dst + C) = make_float2(a0 * scale, a1 * scale);
-                *reinterpret_cast<float2 *>(dst + 2 * C) = make_float2(c0, c1);
+                const float4 l4 = *reinterpret_cast<const float4 *>(&ld_lds[w][0][8 * g + 4 * hf]);
+                const float4 d4 = *reinterpret_cast<const float4 *>(&ld_lds[w][1][8 * g + 4 * hf]);
+                const float lj[4] = {l4.x, l4.y, l4.z, l4.w};
+                const float dj[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+                {
+                    const int r = 4 * g + jj;
+                    const int qrow = q0 + 8 * g + 4 * hf + jj;  // = q0 + row(r, hf)
+                    const bool keep = (k0 + n <= qrow) && (qrow < T);
+                    const float p = fast_exp2(s[r] * c2 - lj[jj]);
+                    s[r] = keep ? p : 0.f;
+                    dp[r] = keep ? p * (dp[r] - dj[jj]) : 0.f;
+                }
             }
+            // dS tile, query-major (row = query, column = key)
+            {
+                float *tile = ws + ds_tile(i, j);
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    tile[mfma_row(r, hf) * 32 + n] = dp[r];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // dV += P^T dO and dK += dS^T Q; step st contracts query
+            // q0 + row(st, hf), the query of accumulator register st. B
+            // operands dO / Q[q0 + row(st, hf)][2n, 2n + 1], loaded four steps
+            // at a time, one chunk ahead.
+            {
+                const uint32_t go = (uint32_t)(q0 + 4 * hf) * Cb + 8u * n;
+                const uint32_t qo = (uint32_t)(q0 + 4 * hf) * Wb + 8u * n;
+                float2 gb[2][4], qb2[2][4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                {
+                    gb[0][e] = bload2(ro, go + (uint32_t)e * Cb);
+                    qb2[0][e] = bload2(rq, qo + (uint32_t)e * Wb);
+                }
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                {
+                    if (c < 3)
+                    {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                        {
+                            // step 4(c+1) + e is query row 8(c+1) + 4hf + e
+                            gb[(c + 1) & 1][e] = bload2(ro, go + (uint32_t)(8 * (c + 1) + e) * Cb);
+                            qb2[(c + 1) & 1][e] = bload2(rq, qo + (uint32_t)(8 * (c + 1) + e) * Wb);
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                    {
+                        const int st = 4 * c + e;
+                        const float2 g2 = gb[c & 1][e], q2 = qb2[c & 1][e];
+                        dv0 = mfma32(s[st], g2.x, dv0);
+                        dv1 = mfma32(s[st], g2.y, dv1);
+                        dk0 = mfma32(dp[st], q2.x, dk0);
+                        dk1 = mfma32(dp[st], q2.y, dk1);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            wave_lds_sync();
         }
-    }
-    else
-    {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
+
+        reduce4(dk0, dk1, dv0, dv1, red, w, lane);
+        if (w == 0)
         {
-            const int key = k0 + mfma_row(r, hf);
-            if (key < T)
+            // register r of lane (n, hf): key k0 + row(r, hf), dims 2n, 2n + 1
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
             {
-                float *dst = grad_x + ((long)b * T + key) * W + (long)h * 64 + 2 * n;
-                *reinterpret_cast<float2 *>(dst + C) = make_float2(dk0[r] * scale, dk1[r] * scale);
-                *reinterpret_cast<float2 *>(dst + 2 * C) = make_float2(dv0[r], dv1[r]);
+                const int key = k0 + mfma_row(r, hf);
+                if (key < T)
+                {
+                    float *dst = gx + (long)key * 3 * C + 2 * n;
+                    *reinterpret_cast<float2 *>(dst + C) = make_float2(dk0[r] * scale, dk1[r] * scale);
+                    *reinterpret_cast<float2 *>(dst + 2 * C) = make_float2(dv0[r], dv1[r]);
+                }
             }
         }
     }
 }
 
-// dQ_i = scale * sum_{j<=i} dS_ij K_j, one wave per (b, h, query block i),
-// query blocks from the last (most key blocks) to the first.
-__global__ __launch_bounds__(64) void bwd_dq_d64_kernel(float *__restrict__ grad_x,
-                                                        const float *__restrict__ dsw,
-                                                        const float *__restrict__ qkv,
-                                                        int T, int C, int H, int bh0, int BHc, int n_qb,
-                                                        float scale)
+// dQ_i = scale * sum_{j<=i} dS_ij K_j. One workgroup per (b, h, query-block
+// pair (n - 1 - p, p)), n + 1 units; per query block the 4 waves split its key
+// blocks round-robin (rotated per workgroup) and their partial dQ are summed
+// through LDS in a fixed order; wave 0 stores.
+__global__ __launch_bounds__(256) void bwd_dq_d64_kernel(float *__restrict__ grad_x,
+                                                         const float *__restrict__ dsw,
+                                                         const float *__restrict__ qkv,
+                                                         int T, int C, int H, int bh0, int BHc, int n_qb,
+                                                         float scale)
 {
-    const int lane = threadIdx.x, n = lane & 31, hf = lane >> 5;
-    const int i = n_qb - 1 - (int)(blockIdx.x / BHc);
+    constexpr int NW = 4;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int n = lane & 31, hf = lane >> 5;
+    const int pr = (int)(blockIdx.x / BHc);
     const int bhl = (int)(blockIdx.x % BHc), bh = bh0 + bhl;
     const int b = bh / H, h = bh % H;
-    const long W = 3L * C;
-    const float *kb = qkv + (long)b * T * W + C + (long)h * 64;
+    const uint32_t Wb = 12u * (uint32_t)C;
+    const rsrc_t rk = make_rsrc(qkv + (long)b * T * 3L * C + C + (long)h * 64,
+                                (uint32_t)(((long)T * 3 * C - C - (long)h * 64) * 4));
     const float *ws = dsw + (long)bhl * ((long)n_qb * (n_qb + 1) / 2) * 1024;
+    float *gx = grad_x + (long)b * T * 3L * C + (long)h * 64;
+    __shared__ float red[2][32][64];
 
-    // dQ[q][d] += dS[q][key] K[key][d]: step t of half hf contracts key
-    // 16 hf + t of the block. A operand dS[n][16 hf + t] (16 contiguous floats
-    // of the tile row), B operand K[key][2n, 2n + 1].
-    v16f a0 = zero16(), a1 = zero16();
-    for (int j = 0; j <= i; ++j)
+    for (int it = 0; it < 2; ++it)
     {
-        const float4 *tile = reinterpret_cast<const float4 *>(ws + ds_tile(i, j) + n * 32 + 16 * hf);
-        float4 d4[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            d4[u] = tile[u];
-        const float dsr[16] = {d4[0].x, d4[0].y, d4[0].z, d4[0].w, d4[1].x, d4[1].y, d4[1].z, d4[1].w,
-                               d4[2].x, d4[2].y, d4[2].z, d4[2].w, d4[3].x, d4[3].y, d4[3].z, d4[3].w};
-        const int kbase = 32 * j + 16 * hf;
-#pragma unroll
-        for (int t = 0; t < 16; ++t)
+        const int i = it == 0 ? n_qb - 1 - pr : pr;
+        if (it == 1 && i == n_qb - 1 - pr)
+            break;
+        const int rot = (pr + (it == 0 ? 0 : n_qb - pr)) % NW;
+        const int j0 = (w - rot + NW) % NW;
+
+        // dQ[q][d] += dS[q][key] K[key][d]: step t of half hf contracts key
+        // 16 hf + t of the block. A operand dS[n][16 hf + t] (16 contiguous
+        // floats of the tile row), B operand K[key][2n, 2n + 1].
+        v16f a0 = zero16(), a1 = zero16();
+        for (int j = j0; j <= i; j += NW)
         {
-            const float2 k2 = *reinterpret_cast<const float2 *>(kb + (long)min(kbase + t, T - 1) * W + 2 * n);
-            a0 = mfma32(dsr[t], k2.x, a0);
-            a1 = mfma32(dsr[t], k2.y, a1);
-        }
-    }
-    // register r of lane (n, hf): dQ[32 i + row(r, hf)][2n, 2n + 1]
+            const float4 *tile = reinterpret_cast<const float4 *>(ws + ds_tile(i, j) + n * 32 + 16 * hf);
+            float4 d4[4];
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-    {
-        const int row = 32 * i + mfma_row(r, hf);
-        if (row < T)
-            *reinterpret_cast<float2 *>(grad_x + ((long)b * T + row) * W + (long)h * 64 + 2 * n) =
-                make_float2(a0[r] * scale, a1[r] * scale);
+            for (int u = 0; u < 4; ++u)
+                d4[u] = tile[u];
+            const float dsr[16] = {d4[0].x, d4[0].y, d4[0].z, d4[0].w, d4[1].x, d4[1].y, d4[1].z, d4[1].w,
+                                   d4[2].x, d4[2].y, d4[2].z, d4[2].w, d4[3].x, d4[3].y, d4[3].z, d4[3].w};
+            const uint32_t kb = (uint32_t)(32 * j + 16 * hf) * Wb + 8u * n;
+#pragma unroll
+            for (int t = 0; t < 16; ++t)
+            {
+                const float2 k2 = bload2(rk, kb + (uint32_t)t * Wb);
+                a0 = mfma32(dsr[t], k2.x, a0);
+                a1 = mfma32(dsr[t], k2.y, a1);
+            }
+        }
+        // (w0 + w1) + (w2 + w3)
+        if (w & 1)
+        {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+            {
+                red[w >> 1][r][lane] = a0[r];
+                red[w >> 1][16 + r][lane] = a1[r];
+            }
+        }
+        __syncthreads();
+        if (!(w & 1))
+        {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+            {
+                a0[r] += red[w >> 1][r][lane];
+                a1[r] += red[w >> 1][16 + r][lane];
+            }
+        }
+        __syncthreads();
+        if (w == 2)
+        {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+            {
+                red[0][r][lane] = a0[r];
+                red[0][16 + r][lane] = a1[r];
+            }
+        }
+        __syncthreads();
+        if (w == 0)
+        {
+            // register r of lane (n, hf): dQ[32 i + row(r, hf)][2n, 2n + 1]
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+            {
+                const int row = 32 * i + mfma_row(r, hf);
+                if (row < T)
+                    *reinterpret_cast<float2 *>(gx + (long)row * 3 * C + 2 * n) =
+                        make_float2((a0[r] + red[0][r][lane]) * scale, (a1[r] + red[0][16 + r][lane]) * scale);
+            }
+        }
+        __syncthreads();  // red is reused by the next query block
     }
 }
 
@@ -484,7 +626,6 @@ size_t bwd_d64_workspace_bytes(const Shape &s, int *bh_per_chunk)
 hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
                           const float *qkv, float *ws, int bh_per_chunk, const Shape &s, hipStream_t st)
 {
-    constexpr int NW = 4;
     const long rows = (long)s.B * s.T;
     hipLaunchKernelGGL(bwd_rowdot_d64_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, D, dy, y,
                        rows, s.H);
@@ -497,10 +638,10 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
     for (int bh0 = 0; bh0 < BH; bh0 += bh_per_chunk)
     {
         const int cnt = BH - bh0 < bh_per_chunk ? BH - bh0 : bh_per_chunk;
-        const unsigned blocks = (unsigned)((long)n_qb * cnt);
-        hipLaunchKernelGGL((bwd_dkdv_d64_kernel<NW>), dim3(blocks), dim3(NW * 64), 0, st, grad_x, ws, lse, D, dy,
-                           qkv, s.T, s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale);
-        hipLaunchKernelGGL(bwd_dq_d64_kernel, dim3(blocks), dim3(64), 0, st, grad_x, ws, qkv, s.T, s.C, s.H, bh0,
+        const unsigned blocks = (unsigned)((long)((n_qb + 1) / 2) * cnt);  // heavy/light pairs
+        hipLaunchKernelGGL(bwd_dkdv_d64_kernel, dim3(blocks), dim3(256), 0, st, grad_x, ws, lse, D, dy, qkv, s.T,
+                           s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale);
+        hipLaunchKernelGGL(bwd_dq_d64_kernel, dim3(blocks), dim3(256), 0, st, grad_x, ws, qkv, s.T, s.C, s.H, bh0,
                            cnt, n_qb, scale);
         e = hipGetLastError();
         if (e != hipSuccess)
