@@ -11,13 +11,26 @@ value = algorithmic FLOPs / GPU time, FLOPs = 12 * 7 * B * H * d * T * (T+1)
 including the diagonal; exp and masking not counted).
 
 Also reported:
-  roofline      the backward op (the dominant cost), timed live with HIP
-                events on the stream its kernels are launched on
+  kernels       per-kernel average durations over the timed region, from the
+                library's launch timer (a HIP event pair recorded on the launch
+                stream around every kernel, gpt_hip_attn_timing_*)
+  roofline      the dominant kernel (most GPU time): algorithmic FLOPs per
+                launch / its average launch duration, against 157.3 TFLOP/s;
+                `traffic` = its measured HBM bytes per launch, read from
+                profiles/<kernel>_c3_traffic.json when that file matches the
+                kernel (written by --traffic from two rocprofv3 --pmc runs,
+                FETCH_SIZE and WRITE_SIZE, each scaled by the same counter's
+                reading for a plain device copy of known size)
   cpu_baseline  the reference's own CPUBackend attention (compiled from its
                 sources into oracle/_ref, -O3) on a bounded sample of the
                 same workload, one thread, on this host
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage:
+  python bench.py [--gpus 1] [--steps K] [--warmup W]       the metric line
+  python bench.py --copy-calibration                        256 MiB device copy x5
+                                                            (run under --pmc)
+  python bench.py --traffic KERNEL FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
+      turns rocprofv3 counter_collection CSVs into profiles/KERNEL_c3_traffic.json
 """
 import argparse
 import json
@@ -40,12 +53,70 @@ def attn_flops(b, t, h, d, fwd=True, bwd=True):
     return (2 * pairs if fwd else 0) + (5 * pairs if bwd else 0)
 
 
+# Algorithmic FLOPs of one launch of each head_dim-64 kernel, in units of
+# B*H*d*T(T+1) (= 2 FLOPs x d per causal pair): forward QK^T + PV = 2;
+# dK/dV kernel S + dP + dV + dK = 4; dQ kernel dS K = 1. The D-row kernel does
+# no matrix work (bandwidth-bound: reads dO and O).
+KERNEL_FLOP_UNITS = {"fwd": 2, "bwd_dkdv": 4, "bwd_dq": 1, "bwd_rowdot": 0}
+KERNEL_SYMBOL = {"fwd": "fwd_d64_kernel", "bwd_dkdv": "bwd_dkdv_d64_kernel", "bwd_dq": "bwd_dq_d64_kernel",
+                 "bwd_rowdot": "bwd_rowdot_d64_kernel"}
+COPY_BYTES = 256 << 20
+
+
+def copy_calibration():
+    """A plain device-to-device copy of COPY_BYTES, five times (for --pmc runs)."""
+    import torch
+
+    x = torch.ones(COPY_BYTES // 4, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(5):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "launches": 5}))
+
+
+def _counter_per_dispatch(path, counter, kernel_substr):
+    import csv
+
+    vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(path))
+            if r["Counter_Name"] == counter and kernel_substr in r["Kernel_Name"]]
+    if not vals:
+        names = sorted({r["Kernel_Name"] for r in csv.DictReader(open(path))})
+        raise SystemExit(f"{path}: no {counter} rows for kernels matching {kernel_substr!r}; kernels: {names}")
+    return sum(vals) / len(vals), len(vals)
+
+
+def write_traffic(kernel, fetch_csv, write_csv, copy_fetch_csv, copy_write_csv):
+    """HBM bytes per launch of `kernel` from FETCH_SIZE / WRITE_SIZE (KiB per
+    dispatch), each scaled by expected / measured for the copy kernel."""
+    sym = KERNEL_SYMBOL[kernel]
+    f_kib, nf = _counter_per_dispatch(fetch_csv, "FETCH_SIZE", sym)
+    w_kib, nw = _counter_per_dispatch(write_csv, "WRITE_SIZE", sym)
+    cf_kib, _ = _counter_per_dispatch(copy_fetch_csv, "FETCH_SIZE", "copy")
+    cw_kib, _ = _counter_per_dispatch(copy_write_csv, "WRITE_SIZE", "copy")
+    f_scale = COPY_BYTES / (cf_kib * 1024)
+    w_scale = COPY_BYTES / (cw_kib * 1024)
+    fetch = f_kib * 1024 * f_scale
+    write = w_kib * 1024 * w_scale
+    out = {"kernel": sym, "workload": "one C3 layer: B=16 T=256 H=12 d=64",
+           "fetch_bytes_per_launch": round(fetch), "write_bytes_per_launch": round(write),
+           "hbm_bytes_per_launch": round(fetch + write),
+           "fetch_kib_raw": f_kib, "write_kib_raw": w_kib, "dispatches": [nf, nw],
+           "copy_scale": {"fetch": f_scale, "write": w_scale, "copy_bytes": COPY_BYTES}}
+    path = os.path.join(ROOT, "profiles", f"{kernel}_c3_traffic.json")
+    with open(path, "w") as fh:
+        json.dump(out, fh, indent=1)
+    print(json.dumps(out))
+
+
 def parse():
     ap = argparse.ArgumentParser()
+    ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--traffic", nargs=5, metavar=("KERNEL", "FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"))
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cpu-layers", type=int, default=4,
+    ap.add_argument("--cpu-layers", type=int, default=12,
                     help="layers of the workload timed on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     return ap.parse_args()
@@ -84,6 +155,12 @@ def cpu_baseline(layers: int):
 
 def main():
     args = parse()
+    if args.traffic:
+        write_traffic(*args.traffic)
+        return
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the attention op "
               f"shards per (batch, head) with no communication; run with --gpus 1.", file=sys.stderr)
@@ -130,17 +207,30 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    mk = lambda: [torch.cuda.Event(enable_timing=True) for _ in range(LAYERS)]  # noqa: E731
-    evs = [[mk() for _ in range(4)] for _ in range(args.steps)]
+    # Timed region: exactly K steps between two events, nothing else recorded.
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
-    for k in range(args.steps):
-        step(evs[k])
+    for _ in range(args.steps):
+        step()
     end.record(stream)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
+
+    # Breakdown pass: the same K steps again with an event pair around every op
+    # (torch events) and every kernel launch (the library's launch timer).
+    # Kept out of the timed region because the extra event packets between
+    # back-to-back kernels slow the step down by ~10%.
+    mk = lambda: [torch.cuda.Event(enable_timing=True) for _ in range(LAYERS)]  # noqa: E731
+    evs = [[mk() for _ in range(4)] for _ in range(args.steps)]
+    gpt_amd.timing_enable(True)
+    torch.cuda.synchronize()
+    for k in range(args.steps):
+        step(evs[k])
+    torch.cuda.synchronize()
+    per_kernel = gpt_amd.timing_read()
+    gpt_amd.timing_enable(False)
     fwd_ms = [e[0][i].elapsed_time(e[1][i]) for e in evs for i in range(LAYERS)]
     bwd_ms = [e[2][i].elapsed_time(e[3][i]) for e in evs for i in range(LAYERS)]
 
@@ -154,10 +244,18 @@ def main():
     bwd_tf = bwd_flops / (bwd_avg_ms * 1e-3) / 1e12
     fwd_tf = fwd_flops / (fwd_avg_ms * 1e-3) / 1e12
 
+    kernels = {k: {"avg_us": round(1e3 * ms / n, 3), "launches": n}
+               for k, (ms, n) in per_kernel.items() if n > 0}
+    dom = max((k for k in kernels if k in KERNEL_FLOP_UNITS), key=lambda k: per_kernel[k][0])
+    dom_ms = per_kernel[dom][0] / per_kernel[dom][1]
+    dom_flops = KERNEL_FLOP_UNITS[dom] * B * H * D_HEAD * T * (T + 1)
+    dom_tf = dom_flops / (dom_ms * 1e-3) / 1e12
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "attn_bwd_c3_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", f"{dom}_c3_traffic.json")
     if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
+        rec = json.load(open(tpath))
+        if rec.get("kernel") == KERNEL_SYMBOL[dom]:
+            traffic = rec.get("hbm_bytes_per_launch")
 
     out = {
         "metric": METRIC,
@@ -180,14 +278,17 @@ def main():
         "pct_fp32_mfma_peak": round(100 * tflops / PEAK_FP32_MFMA_TFLOPS, 2),
         "fwd": {"avg_ms": round(fwd_avg_ms, 5), "tflops": round(fwd_tf, 3)},
         "bwd": {"avg_ms": round(bwd_avg_ms, 5), "tflops": round(bwd_tf, 3)},
+        "kernels": kernels,
         "roofline": {
-            "kernel": "attention backward op: bwd_prep_kernel + bwd_d64_kernel<2>",
+            "kernel": KERNEL_SYMBOL[dom],
             "bound": "mfma",
-            "achieved": round(bwd_tf, 3),
+            "achieved": round(dom_tf, 3),
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(bwd_tf / PEAK_FP32_MFMA_TFLOPS, 4),
+            "frac": round(dom_tf / PEAK_FP32_MFMA_TFLOPS, 4),
             "traffic": traffic,
+            "flops_per_launch": dom_flops,
+            "avg_launch_us": round(dom_ms * 1e3, 3),
         },
     }
     if not args.no_cpu:

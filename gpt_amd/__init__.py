@@ -17,4 +17,6 @@ from .attention import (  # noqa: F401
     lib_path,
     load_library,
     set_path,
+    timing_enable,
+    timing_read,
 )

@@ -61,6 +61,10 @@ def load_library():
         lib.gpt_hip_attn_device_ok.restype = i
         lib.gpt_hip_attn_set_path.argtypes = [i]
         lib.gpt_hip_attn_set_path.restype = i
+        lib.gpt_hip_attn_timing_enable.argtypes = [i]
+        lib.gpt_hip_attn_timing_enable.restype = i
+        lib.gpt_hip_attn_timing_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int), i]
+        lib.gpt_hip_attn_timing_read.restype = i
         _lib = lib
     return _lib
 
@@ -142,6 +146,26 @@ def attention_backward(qkv, y, lse, grad_y, num_heads: int, stream=None):
 
 def device_ok() -> bool:
     return bool(load_library().gpt_hip_attn_device_ok())
+
+
+KERNEL_KINDS = ("fwd", "bwd_rowdot", "bwd_dkdv", "bwd_dq", "other")
+
+
+def timing_enable(on: bool = True) -> None:
+    """Start (or stop) recording a HIP event pair around every kernel launch."""
+    _check(load_library().gpt_hip_attn_timing_enable(1 if on else 0))
+
+
+def timing_read() -> dict:
+    """Wait for the recorded launches; return {kind: (total_ms, launches)} and
+    forget them. Kinds are KERNEL_KINDS."""
+    n = len(KERNEL_KINDS)
+    ms = (ctypes.c_double * n)()
+    cnt = (ctypes.c_int * n)()
+    rc = load_library().gpt_hip_attn_timing_read(ms, cnt, n)
+    if rc < 0:
+        _check(rc)
+    return {k: (ms[i], cnt[i]) for i, k in enumerate(KERNEL_KINDS)}
 
 
 def set_path(path: int) -> int:

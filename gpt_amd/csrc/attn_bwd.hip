@@ -627,8 +627,10 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
                           const float *qkv, float *ws, int bh_per_chunk, const Shape &s, hipStream_t st)
 {
     const long rows = (long)s.B * s.T;
+    timer_begin(kKindRowdot, st);
     hipLaunchKernelGGL(bwd_rowdot_d64_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, D, dy, y,
                        rows, s.H);
+    timer_end(st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
@@ -639,10 +641,14 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
     {
         const int cnt = BH - bh0 < bh_per_chunk ? BH - bh0 : bh_per_chunk;
         const unsigned blocks = (unsigned)((long)((n_qb + 1) / 2) * cnt);  // heavy/light pairs
+        timer_begin(kKindDkdv, st);
         hipLaunchKernelGGL(bwd_dkdv_d64_kernel, dim3(blocks), dim3(256), 0, st, grad_x, ws, lse, D, dy, qkv, s.T,
                            s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale);
+        timer_end(st);
+        timer_begin(kKindDq, st);
         hipLaunchKernelGGL(bwd_dq_d64_kernel, dim3(blocks), dim3(256), 0, st, grad_x, ws, qkv, s.T, s.C, s.H, bh0,
                            cnt, n_qb, scale);
+        timer_end(st);
         e = hipGetLastError();
         if (e != hipSuccess)
             return e;
@@ -666,9 +672,13 @@ static void launch_bwd_general_dm(float *grad_x, const float *lse, const float *
 hipError_t launch_bwd_general(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
                               const float *qkv, const Shape &s, hipStream_t st)
 {
+    timer_begin(kKindOther, st);
     hipError_t e = launch_bwd_prep(grad_x, D, dy, y, s, st, 0);
     if (e != hipSuccess)
+    {
+        timer_end(st);
         return e;
+    }
     if (s.d <= 16)
         launch_bwd_general_dm<16>(grad_x, lse, D, dy, qkv, s, st);
     else if (s.d <= 32)
@@ -679,6 +689,7 @@ hipError_t launch_bwd_general(float *grad_x, float *D, const float *lse, const f
         launch_bwd_general_dm<128>(grad_x, lse, D, dy, qkv, s, st);
     else
         launch_bwd_general_dm<256>(grad_x, lse, D, dy, qkv, s, st);
+    timer_end(st);
     return hipGetLastError();
 }
 

@@ -254,13 +254,18 @@ hipError_t launch_bwd_d64_atomic(float *grad_x, float *D, const float *lse, cons
                                  const float *qkv, const Shape &s, hipStream_t st)
 {
     constexpr int QS = 2, BKV = 64 * QS;
+    timer_begin(kKindOther, st);
     hipError_t e = launch_bwd_prep(grad_x, D, dy, y, s, st, 1);
     if (e != hipSuccess)
+    {
+        timer_end(st);
         return e;
+    }
     const int n_kb = (s.T + BKV - 1) / BKV;
     const float scale = softmax_scale(64);
     hipLaunchKernelGGL((bwd_d64_atomic_kernel<QS>), dim3((unsigned)((long)n_kb * s.B * s.H)), dim3(128 * QS), 0,
                        st, grad_x, lse, D, dy, qkv, s.B, s.T, s.C, s.H, scale, scale * kLog2e);
+    timer_end(st);
     return hipGetLastError();
 }
 

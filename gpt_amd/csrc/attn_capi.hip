@@ -62,6 +62,22 @@ int check_device(const char *op)
     return 0;
 }
 
+// Optional launch timer: when enabled, each kernel launch is bracketed by two
+// HIP events recorded on its stream (from a fixed pool, reused after every
+// read); gpt_hip_attn_timing_read() waits for them and sums the elapsed time
+// per kernel kind. Not thread-safe; meant for one benchmarking thread.
+constexpr int kTimerSlots = 8192;
+struct LaunchTimer
+{
+    bool on = false;
+    bool ready = false;
+    int used = 0;
+    int open = -1;
+    hipEvent_t ev0[kTimerSlots], ev1[kTimerSlots];
+    int kind[kTimerSlots];
+};
+LaunchTimer g_timer;
+
 // Stream-ordered dS workspace for the deterministic backward. The device's
 // default memory pool is told to keep freed memory (release threshold = max),
 // so after the first call hipMallocAsync / hipFreeAsync hand the same block
@@ -89,6 +105,29 @@ hipError_t workspace_alloc(void **p, size_t bytes, hipStream_t st)
 }
 
 }  // namespace
+
+namespace gpt_attn {
+
+void timer_begin(int kind, hipStream_t st)
+{
+    LaunchTimer &t = g_timer;
+    if (!t.on || t.used >= kTimerSlots)
+        return;
+    t.open = t.used++;
+    t.kind[t.open] = kind;
+    (void)hipEventRecord(t.ev0[t.open], st);
+}
+
+void timer_end(hipStream_t st)
+{
+    LaunchTimer &t = g_timer;
+    if (!t.on || t.open < 0)
+        return;
+    (void)hipEventRecord(t.ev1[t.open], st);
+    t.open = -1;
+}
+
+}  // namespace gpt_attn
 
 extern "C" {
 
@@ -161,6 +200,54 @@ int gpt_hip_attn_bwd_f32(float *grad_x, float *D_cache, const float *lse, const 
 }
 
 const char *gpt_hip_attn_last_error(void) { return g_err; }
+
+int gpt_hip_attn_timing_enable(int on)
+{
+    LaunchTimer &t = g_timer;
+    if (on && !t.ready)
+    {
+        if (int rc = check_device("gpt_hip_attn_timing_enable"))
+            return rc;
+        for (int i = 0; i < kTimerSlots; ++i)
+        {
+            if (hipEventCreate(&t.ev0[i]) != hipSuccess || hipEventCreate(&t.ev1[i]) != hipSuccess)
+                return fail(GPT_HIP_ATTN_ELAUNCH, "gpt_hip_attn_timing_enable: hipEventCreate failed");
+        }
+        t.ready = true;
+    }
+    t.on = on != 0;
+    t.used = 0;
+    t.open = -1;
+    return 0;
+}
+
+int gpt_hip_attn_timing_read(double *ms, int *count, int n_kinds)
+{
+    LaunchTimer &t = g_timer;
+    if (!ms || !count || n_kinds <= 0)
+        return fail(GPT_HIP_ATTN_ENULL, "gpt_hip_attn_timing_read: NULL output or n_kinds <= 0");
+    for (int k = 0; k < n_kinds; ++k)
+    {
+        ms[k] = 0.0;
+        count[k] = 0;
+    }
+    for (int i = 0; i < t.used; ++i)
+    {
+        if (hipEventSynchronize(t.ev1[i]) != hipSuccess)
+            return fail(GPT_HIP_ATTN_ELAUNCH, "gpt_hip_attn_timing_read: hipEventSynchronize failed");
+        float e = 0.f;
+        if (hipEventElapsedTime(&e, t.ev0[i], t.ev1[i]) != hipSuccess)
+            return fail(GPT_HIP_ATTN_ELAUNCH, "gpt_hip_attn_timing_read: hipEventElapsedTime failed");
+        if (t.kind[i] < n_kinds)
+        {
+            ms[t.kind[i]] += e;
+            count[t.kind[i]] += 1;
+        }
+    }
+    const int n = t.used;
+    t.used = 0;
+    return n;
+}
 
 int gpt_hip_attn_device_ok(void)
 {

@@ -281,8 +281,10 @@ hipError_t launch_fwd_d64(float *y, float *lse, const float *qkv, const Shape &s
     const int BH = s.B * s.H;
     const long blocks = (long)((n_qb + 1) / 2) * BH;  // heavy/light pairs
     const float qscale = softmax_scale(64) * kLog2e;
+    timer_begin(kKindFwd, st);
     hipLaunchKernelGGL((fwd_d64_kernel<NW>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, y, lse, qkv, s.T,
                        s.C, s.H, BH, n_qb, qscale);
+    timer_end(st);
     return hipGetLastError();
 }
 
@@ -291,6 +293,7 @@ hipError_t launch_fwd_general(float *y, float *lse, const float *qkv, const Shap
     const long rows = (long)s.B * s.H * s.T;
     const dim3 grid((unsigned)((rows + 127) / 128)), block(128);
     const float qscale = softmax_scale(s.d) * kLog2e;
+    timer_begin(kKindOther, st);
     if (s.d <= 16)
         hipLaunchKernelGGL(fwd_general_kernel<16>, grid, block, 0, st, y, lse, qkv, s.B, s.T, s.C, s.H, s.d, qscale);
     else if (s.d <= 32)
@@ -301,6 +304,7 @@ hipError_t launch_fwd_general(float *y, float *lse, const float *qkv, const Shap
         hipLaunchKernelGGL(fwd_general_kernel<128>, grid, block, 0, st, y, lse, qkv, s.B, s.T, s.C, s.H, s.d, qscale);
     else
         hipLaunchKernelGGL(fwd_general_kernel<256>, grid, block, 0, st, y, lse, qkv, s.B, s.T, s.C, s.H, s.d, qscale);
+    timer_end(st);
     return hipGetLastError();
 }
 

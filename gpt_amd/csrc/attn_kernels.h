@@ -12,6 +12,22 @@ struct Shape
     int B, T, C, H, d;
 };
 
+// Kernel kinds reported by the optional launch timer (gpt_hip_attn_timing_*).
+enum KernelKind
+{
+    kKindFwd = 0,       // fwd_d64_kernel
+    kKindRowdot = 1,    // bwd_rowdot_d64_kernel
+    kKindDkdv = 2,      // bwd_dkdv_d64_kernel
+    kKindDq = 3,        // bwd_dq_d64_kernel
+    kKindOther = 4,     // general-d kernels, atomic-variant kernels
+    kNumKinds = 5
+};
+
+// Brackets the launches between begin and end with HIP events on `st` when the
+// timer is enabled; no-ops otherwise.
+void timer_begin(int kind, hipStream_t st);
+void timer_end(hipStream_t st);
+
 // Largest dS workspace one backward call asks for; bigger problems are
 // processed in chunks of (b, h) pairs that fit.
 constexpr size_t kWorkspaceCap = size_t(2) << 30;

@@ -82,6 +82,19 @@ const char *gpt_hip_attn_last_error(void);
  * (the reference assumes a device). */
 int gpt_hip_attn_device_ok(void);
 
+/* Launch timer, for benchmarks and tracing. gpt_hip_attn_timing_enable(1)
+ * makes every later kernel launch of the library record a HIP event pair on
+ * its stream (up to 8192 launches between reads); (0) turns it off.
+ * gpt_hip_attn_timing_read() waits for the recorded events, writes the summed
+ * milliseconds and the launch count per kernel kind into ms[k] / count[k] for
+ * k < n_kinds, forgets the recorded launches and returns how many there were.
+ * Kinds: 0 head_dim-64 forward, 1 backward D rows, 2 backward dK/dV (+ dS
+ * tiles), 3 backward dQ, 4 everything else (general-d kernels, the atomic
+ * variant). Not thread-safe. No reference counterpart (the reference times
+ * whole training steps with a host clock, src/core/benchmark.h:5-16). */
+int gpt_hip_attn_timing_enable(int on);
+int gpt_hip_attn_timing_read(double *ms, int *count, int n_kinds);
+
 /* Kernel selection, for tests and tuning only (not thread-safe; process-wide).
  *   path 0  automatic (default): MFMA kernels for head_dim 64, general-d
  *           kernels otherwise

@@ -98,3 +98,10 @@ def test_python_wrapper_rejects_host_tensors():
     x = torch.zeros(1, 4, 192)
     with pytest.raises(ValueError):
         gpt_amd.attention_forward(x, 3)
+
+
+def test_timing_without_device_is_an_error():
+    if gpt_amd.device_ok():
+        pytest.skip("a HIP device is present")
+    assert gpt_amd.load_library().gpt_hip_attn_timing_enable(1) == ENODEV
+    assert gpt_amd.timing_read() == {k: (0.0, 0) for k in gpt_amd.attention.KERNEL_KINDS}

@@ -256,3 +256,24 @@ def test_batch_slices_are_independent(dev):
     for b in range(B):
         yb, lb = gpu_fwd(dev, np.ascontiguousarray(x[b:b + 1]), H)
         assert np.array_equal(yb, y[b:b + 1]) and np.array_equal(lb, lse[b:b + 1])
+
+
+def test_launch_timer_counts_each_kernel(dev):
+    import torch
+
+    B, T, C, H = 2, 100, 768, 12
+    x = _to(dev, synth.qkv(B, T, C, 51))
+    g = _to(dev, synth.grad_out(B, T, C, 51))
+    gpt_amd.timing_enable(True)
+    try:
+        y, lse = gpt_amd.attention_forward(x, H)
+        gpt_amd.attention_backward(x, y, lse, g, H)
+        torch.cuda.synchronize()
+        t = gpt_amd.timing_read()
+    finally:
+        gpt_amd.timing_enable(False)
+    for k in ("fwd", "bwd_rowdot", "bwd_dkdv", "bwd_dq"):
+        ms, n = t[k]
+        assert n == 1 and ms > 0, (k, t[k])
+    assert t["other"] == (0.0, 0)
+    assert gpt_amd.timing_read()["fwd"] == (0.0, 0)  # read forgets
