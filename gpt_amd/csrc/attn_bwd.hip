@@ -184,13 +184,26 @@ __device__ __forceinline__ void reduce4(v16f &v0, v16f &v1, v16f &v2, v16f &v3, 
 // kRowStride) and the 4 waves split its query blocks round-robin (rotated per
 // workgroup), accumulating partial dK / dV in registers that are summed
 // through LDS in a fixed order and stored by wave 0.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void bwd_dkdv_d64_kernel(
+//
+// Per unit (query block i) a wave runs two MFMA phases:
+//   phase 1  S = Q K^T, dP = dO V^T: 8 chunks of 4 + 4 MFMAs; A operands
+//            Q / dO[q0 + n][32 hf + 4c ..] (one float4 each per chunk, from
+//            L2), B operands K / V from LDS
+//   phase 2  dV += P^T dO, dK += dS^T Q: 8 chunks of 2 steps x 4 MFMAs; B
+//            operands dO / Q[q0 + row(st, hf)][2n, 2n + 1] (float2, from L2)
+// Every global operand is loaded one chunk ahead, and the first chunk of each
+// phase one phase ahead: phase 2's while P and dS are formed, the next unit's
+// phase 1 (and its lse / D rows) during this unit's phase 2. All row and block
+// offsets are wave-uniform and go in the buffer loads' scalar offset; rows past
+// T read as zeros through the buffer range check. 3 waves per SIMD keep all
+// workgroups of a B=16, T=256, H=12 call resident at once.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void bwd_dkdv_d64_kernel(
     float *__restrict__ grad_x, float *__restrict__ dsw, const float *__restrict__ lse,
     const float *__restrict__ Dv, const float *__restrict__ dy, const float *__restrict__ qkv, int T, int C, int H,
     int bh0, int BHc, int n_qb, float c2, float scale)
 {
     constexpr int NW = 4, ST = kRowStride;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int n = lane & 31, hf = lane >> 5;
     const int pr = (int)(blockIdx.x / BHc);
     const int bhl = (int)(blockIdx.x % BHc), bh = bh0 + bhl;
@@ -204,6 +217,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
     float *ws = dsw + (long)bhl * ((long)n_qb * (n_qb + 1) / 2) * 1024;
     float *gx = grad_x + (long)b * T * 3L * C + (long)h * 64;
 
+    // lane-dependent parts of the operand offsets (bytes)
+    const uint32_t q1_lane = (uint32_t)n * Wb + 128u * hf;      // phase 1: Q[n][32 hf ..]
+    const uint32_t o1_lane = (uint32_t)n * Cb + 128u * hf;      // phase 1: dO[n][32 hf ..]
+    const uint32_t q2_lane = 4u * hf * Wb + 8u * (uint32_t)n;   // phase 2: Q[4 hf + ..][2n ..]
+    const uint32_t o2_lane = 4u * hf * Cb + 8u * (uint32_t)n;   // phase 2: dO[4 hf + ..][2n ..]
+    const uint32_t l_lane = (uint32_t)n * Hb;                    // lse / D row n
+
     __shared__ __attribute__((aligned(16))) float kv_lds[2][32 * ST];  // K, V of the key block
     __shared__ __attribute__((aligned(16))) float ld_lds[NW][2][32];   // per wave: L * log2(e), D
     __shared__ float red[2][64][64];
@@ -214,81 +234,85 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
         if (it == 1 && j == pr)
             break;  // odd n_qb: the middle key block has no partner
         const int k0 = 32 * j;
+        // wave w takes query blocks i = j + u with (u + rot) % NW == w
+        const int rot = (pr + (it == 0 ? 0 : n_qb - pr)) % NW;
+        const int i_first = j + (w - rot + NW) % NW;
+
+        // first unit's phase-1 chunk 0 and lse / D rows, in flight while K / V
+        // are staged
+        float4 qa[2], oa[2];
+        float lrow, drow;
+        {
+            const uint32_t rq0 = i_first < n_qb ? 32u * (uint32_t)i_first * Wb : kNoBlock;
+            const uint32_t ro0 = i_first < n_qb ? 32u * (uint32_t)i_first * Cb : kNoBlock;
+            const uint32_t rl0 = i_first < n_qb ? 32u * (uint32_t)i_first * Hb : kNoBlock;
+            qa[0] = bload4s(rq, q1_lane, rq0);
+            oa[0] = bload4s(ro, o1_lane, ro0);
+            lrow = bload1s(rl, l_lane, rl0);
+            drow = bload1s(rd, l_lane, rl0);
+        }
+
         __syncthreads();  // the previous key block's LDS reads are done
 #pragma unroll
         for (int u = 0; u < 4; ++u)
         {
             const int idx = tid + 256 * u, which = idx >> 9, r = (idx >> 4) & 31, c4 = idx & 15;
-            const float4 v = bload4(rq, (uint32_t)(k0 + r) * Wb + (1u + which) * Cb + 16u * c4);
+            const float4 v = bload4s(rq, (uint32_t)r * Wb + (1u + which) * Cb + 16u * c4, (uint32_t)k0 * Wb);
             *reinterpret_cast<float4 *>(&kv_lds[which][r * ST + 4 * c4]) = v;
         }
         __syncthreads();
 
-        // wave w takes query blocks i = j + u with (u + rot) % NW == w
-        const int rot = (pr + (it == 0 ? 0 : n_qb - pr)) % NW;
-        const int u0 = (w - rot + NW) % NW;
+        const float *kr = &kv_lds[0][n * ST + 32 * hf];
+        const float *vr = &kv_lds[1][n * ST + 32 * hf];
         v16f dk0 = zero16(), dk1 = zero16(), dv0 = zero16(), dv1 = zero16();
-        for (int i = j + u0; i < n_qb; i += NW)
+        for (int i = i_first; i < n_qb; i += NW)
         {
             const int q0 = 32 * i;
+            const bool more = i + NW < n_qb;
+            const uint32_t rqn = more ? 32u * (uint32_t)(i + NW) * Wb : kNoBlock;
+            const uint32_t ron = more ? 32u * (uint32_t)(i + NW) * Cb : kNoBlock;
+            const uint32_t rln = more ? 32u * (uint32_t)(i + NW) * Hb : kNoBlock;
             if (hf == 0)
             {
-                ld_lds[w][0][n] = bload1(rl, (uint32_t)(q0 + n) * Hb) * kLog2e;
-                ld_lds[w][1][n] = bload1(rd, (uint32_t)(q0 + n) * Hb);
+                ld_lds[w][0][n] = lrow * kLog2e;
+                ld_lds[w][1][n] = drow;
             }
-            // S[query q0 + row(r)][key k0 + n] and dP likewise. A operands
-            // Q / dO[q0 + n][32 hf + s] (global), B operands K / V[k0 + n][32 hf + s]
-            // (LDS).
-            // Four chunks of two float4 each; chunk c + 1's loads are issued
-            // before chunk c's MFMAs (two register buffers in flight).
+
+            // phase 1: S[query q0 + row(r)][key k0 + n], dP likewise
             v16f s = zero16(), dp = zero16();
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
             {
-                const uint32_t qo = (uint32_t)(q0 + n) * Wb + 128u * hf;
-                const uint32_t oo = (uint32_t)(q0 + n) * Cb + 128u * hf;
-                const float *kr = &kv_lds[0][n * ST + 32 * hf];
-                const float *vr = &kv_lds[1][n * ST + 32 * hf];
-                float4 qa[2][2], oa[2][2];
-#pragma unroll
-                for (int e = 0; e < 2; ++e)
+                if (c < 7)
                 {
-                    qa[0][e] = bload4(rq, qo + 16u * e);
-                    oa[0][e] = bload4(ro, oo + 16u * e);
+                    qa[(c + 1) & 1] = bload4s(rq, q1_lane + 16u * (c + 1), (uint32_t)q0 * Wb);
+                    oa[(c + 1) & 1] = bload4s(ro, o1_lane + 16u * (c + 1), (uint32_t)q0 * Cb);
                 }
+                __builtin_amdgcn_sched_barrier(0);
+                const float4 q4 = qa[c & 1], o4 = oa[c & 1];
+                const float4 kb = *reinterpret_cast<const float4 *>(kr + 4 * c);
+                const float4 vb = *reinterpret_cast<const float4 *>(vr + 4 * c);
+                s = mfma32(q4.x, kb.x, s);
+                dp = mfma32(o4.x, vb.x, dp);
+                s = mfma32(q4.y, kb.y, s);
+                dp = mfma32(o4.y, vb.y, dp);
+                s = mfma32(q4.z, kb.z, s);
+                dp = mfma32(o4.z, vb.z, dp);
+                s = mfma32(q4.w, kb.w, s);
+                dp = mfma32(o4.w, vb.w, dp);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+
+            // phase 2's chunk 0 (query rows 4 hf + {0, 1}), in flight while P and
+            // dS are formed
+            float2 gb[2][2], qb[2][2];
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                {
-                    if (c < 3)
-                    {
-#pragma unroll
-                        for (int e = 0; e < 2; ++e)
-                        {
-                            qa[(c + 1) & 1][e] = bload4(rq, qo + 16u * (2 * c + 2 + e));
-                            oa[(c + 1) & 1][e] = bload4(ro, oo + 16u * (2 * c + 2 + e));
-                        }
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int e = 0; e < 2; ++e)
-                    {
-                        const int t = 2 * c + e;
-                        const float4 q4 = qa[c & 1][e], o4 = oa[c & 1][e];
-                        const float4 kb = *reinterpret_cast<const float4 *>(kr + 4 * t);
-                        const float4 vb = *reinterpret_cast<const float4 *>(vr + 4 * t);
-                        s = mfma32(q4.x, kb.x, s);
-                        dp = mfma32(o4.x, vb.x, dp);
-                        s = mfma32(q4.y, kb.y, s);
-                        dp = mfma32(o4.y, vb.y, dp);
-                        s = mfma32(q4.z, kb.z, s);
-                        dp = mfma32(o4.z, vb.z, dp);
-                        s = mfma32(q4.w, kb.w, s);
-                        dp = mfma32(o4.w, vb.w, dp);
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                }
+            for (int e = 0; e < 2; ++e)
+            {
+                gb[0][e] = bload2s(ro, o2_lane, (uint32_t)(q0 + e) * Cb);
+                qb[0][e] = bload2s(rq, q2_lane, (uint32_t)(q0 + e) * Wb);
             }
             wave_lds_sync();
-            // Phase boundaries keep the scheduler from hoisting the next
-            // phase's loads into this one (register pressure -> occupancy).
             __builtin_amdgcn_sched_barrier(0);
             // P and dS (without the 1/sqrt(d)); zero where key > query or the
             // query row is past T.
@@ -312,52 +336,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
             }
             // dS tile, query-major (row = query, column = key)
             {
-                float *tile = ws + ds_tile(i, j);
+                float *tile = ws + ds_tile(i, j) + (4 * hf) * 32 + n;
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    tile[mfma_row(r, hf) * 32 + n] = dp[r];
+                    tile[(8 * (r >> 2) + (r & 3)) * 32] = dp[r];
             }
             __builtin_amdgcn_sched_barrier(0);
-            // dV += P^T dO and dK += dS^T Q; step st contracts query
-            // q0 + row(st, hf), the query of accumulator register st. B
-            // operands dO / Q[q0 + row(st, hf)][2n, 2n + 1], loaded four steps
-            // at a time, one chunk ahead.
+
+            // phase 2: step st contracts query q0 + row(st, hf), the query of
+            // accumulator register st; chunk c = steps 2c, 2c + 1
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
             {
-                const uint32_t go = (uint32_t)(q0 + 4 * hf) * Cb + 8u * n;
-                const uint32_t qo = (uint32_t)(q0 + 4 * hf) * Wb + 8u * n;
-                float2 gb[2][4], qb2[2][4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
+                if (c < 7)
                 {
-                    gb[0][e] = bload2(ro, go + (uint32_t)e * Cb);
-                    qb2[0][e] = bload2(rq, qo + (uint32_t)e * Wb);
-                }
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
+                    for (int e = 0; e < 2; ++e)
+                    {
+                        const int st = 2 * (c + 1) + e;
+                        const uint32_t row = (uint32_t)(q0 + 8 * (st >> 2) + (st & 3));
+                        gb[(c + 1) & 1][e] = bload2s(ro, o2_lane, row * Cb);
+                        qb[(c + 1) & 1][e] = bload2s(rq, q2_lane, row * Wb);
+                    }
+                }
+                if (c == 3)
                 {
-                    if (c < 3)
-                    {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                        {
-                            // step 4(c+1) + e is query row 8(c+1) + 4hf + e
-                            gb[(c + 1) & 1][e] = bload2(ro, go + (uint32_t)(8 * (c + 1) + e) * Cb);
-                            qb2[(c + 1) & 1][e] = bload2(rq, qo + (uint32_t)(8 * (c + 1) + e) * Wb);
-                        }
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                    {
-                        const int st = 4 * c + e;
-                        const float2 g2 = gb[c & 1][e], q2 = qb2[c & 1][e];
-                        dv0 = mfma32(s[st], g2.x, dv0);
-                        dv1 = mfma32(s[st], g2.y, dv1);
-                        dk0 = mfma32(dp[st], q2.x, dk0);
-                        dk1 = mfma32(dp[st], q2.y, dk1);
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
+                    // next unit's phase-1 chunk 0 and lse / D rows
+                    qa[0] = bload4s(rq, q1_lane, rqn);
+                    oa[0] = bload4s(ro, o1_lane, ron);
+                    lrow = bload1s(rl, l_lane, rln);
+                    drow = bload1s(rd, l_lane, rln);
                 }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                {
+                    const int st = 2 * c + e;
+                    const float2 g2 = gb[c & 1][e], q2 = qb[c & 1][e];
+                    dv0 = mfma32(s[st], g2.x, dv0);
+                    dv1 = mfma32(s[st], g2.y, dv1);
+                    dk0 = mfma32(dp[st], q2.x, dk0);
+                    dk1 = mfma32(dp[st], q2.y, dk1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
             wave_lds_sync();
         }

@@ -34,6 +34,11 @@ int fail(int code, const char *fmt, ...)
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The head_dim-64 kernels address one batch slice of qkv through a 32-bit
+// buffer range and use offsets at or above 2^31 as "no block"; larger slices
+// take the general-d kernels.
+bool slice_fits_buffer(const gpt_attn::Shape &s) { return (long long)s.T * 3LL * s.C * 4LL < (1LL << 31); }
+
 int check_shape(const char *op, int B, int T, int C, int H, gpt_attn::Shape *s)
 {
     if (B < 0 || T < 0 || C <= 0 || H <= 0)
@@ -145,7 +150,7 @@ int gpt_hip_attn_fwd_f32(float *y, float *lse, const float *qkv, int batch_size,
     if (int rc = check_device(op))
         return rc;
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const bool mfma = g_path != 1 && s.d == 64 && aligned16(y) && aligned16(qkv);
+    const bool mfma = g_path != 1 && s.d == 64 && slice_fits_buffer(s) && aligned16(y) && aligned16(qkv);
     const hipError_t e = mfma ? gpt_attn::launch_fwd_d64(y, lse, qkv, s, st)
                               : gpt_attn::launch_fwd_general(y, lse, qkv, s, st);
     if (e != hipSuccess)
@@ -168,8 +173,8 @@ int gpt_hip_attn_bwd_f32(float *grad_x, float *D_cache, const float *lse, const 
     if (int rc = check_device(op))
         return rc;
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const bool mfma = g_path != 1 && s.d == 64 && aligned16(grad_x) && aligned16(grad_y) && aligned16(y) &&
-                      aligned16(qkv);
+    const bool mfma = g_path != 1 && s.d == 64 && slice_fits_buffer(s) && aligned16(grad_x) &&
+                      aligned16(grad_y) && aligned16(y) && aligned16(qkv);
     if (!mfma)
     {
         const hipError_t e = gpt_attn::launch_bwd_general(grad_x, D_cache, lse, grad_y, y, qkv, s, st);

@@ -83,6 +83,13 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes)
 {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
+// Buffer offset used for a block that does not exist: past the end of every
+// buffer range the kernels build (the host only takes the buffer-load kernels
+// for tensors below 2^31 bytes per batch slice, and lane offsets inside a
+// block stay far below 2^31), so such a load returns zeros and touches no
+// memory. Lets software-pipelined loops issue the same loads every iteration.
+constexpr uint32_t kNoBlock = 0x80000000u;
+
 __device__ __forceinline__ float4 bload4(rsrc_t r, uint32_t off)
 {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
@@ -97,6 +104,28 @@ __device__ __forceinline__ float bload1(rsrc_t r, uint32_t off)
 {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
 }
+
+// The same loads with a wave-uniform part of the offset in an SGPR (soffset).
+// gfx950's range check applies to voffset + soffset + the immediate, so rows
+// past the range still read as zeros, and block / row bases cost no VGPRs.
+__device__ __forceinline__ float4 bload4s(rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+}
+__device__ __forceinline__ float2 bload2s(rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+}
+__device__ __forceinline__ float bload1s(rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+
+// Index of the calling wave in its workgroup, as a value the compiler knows
+// to be wave-uniform (so offsets derived from it can live in SGPRs).
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 __device__ __forceinline__ v16f zero16()
 {

@@ -46,7 +46,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(3))) vo
                                                           int T, int C, int H, int BH, int n_qb,
                                                           float qscale)
 {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int n = lane & 31, hf = lane >> 5;
     const int pr = (int)(blockIdx.x / BH);
     const int bh = (int)(blockIdx.x % BH);
@@ -88,19 +88,30 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(3))) vo
         v16f o0 = zero16(), o1 = zero16();  // O^T rows d = 2 * row + 0 / + 1
         float m = -INFINITY, l = 0.f;       // running max (log2 units) and sum
 
-        for (int j = j0; j <= qb; j += NW)
+        // Software pipeline over this wave's key blocks j0, j0 + NW, ...:
+        // K of the next block is loaded while this block's softmax and PV run,
+        // V of the next block while the next block's S^T runs. A block that
+        // does not exist is "loaded" from offset kNoBlock, past the end of the
+        // buffer range: the hardware returns zeros without touching memory,
+        // so every iteration issues the same loads and no wait depends on a
+        // branch.
+        // A operands: K[32j + n][32 hf + s] for S^T, and for step st of
+        // O^T += V^T P^T, V[32j + row(st, hf)][2n, 2n + 1].
+        float4 kv[8];
+        float2 vv[16];
         {
-            const uint32_t kb = 32u * (uint32_t)j * Wb;
-            // A operands: K[32j + n][32 hf + s] for S^T, and for step st of
-            // O^T += V^T P^T, V[32j + row(st, hf)][2n, 2n + 1]
-            float4 kv[8];
+            const uint32_t kb = j0 <= qb ? 32u * (uint32_t)j0 * Wb : kNoBlock;
 #pragma unroll
             for (int t = 0; t < 8; ++t)
-                kv[t] = bload4(rs, kb + k_lane + 16u * t);
-            float2 vv[16];
+                kv[t] = bload4s(rs, k_lane + 16u * t, kb);
 #pragma unroll
             for (int st = 0; st < 16; ++st)
-                vv[st] = bload2(rs, kb + (uint32_t)(8 * (st >> 2) + (st & 3)) * Wb + v_lane);
+                vv[st] = bload2s(rs, v_lane, kb + (uint32_t)(8 * (st >> 2) + (st & 3)) * Wb);
+        }
+
+        for (int j = j0; j <= qb; j += NW)
+        {
+            const uint32_t kn = j + NW <= qb ? 32u * (uint32_t)(j + NW) * Wb : kNoBlock;
 
             // S^T[key 32j + row(r)][query q0 + n], in log2 units
             v16f s = zero16();
@@ -112,6 +123,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(3))) vo
                 s = mfma32(kv[t].z, qreg[4 * t + 2], s);
                 s = mfma32(kv[t].w, qreg[4 * t + 3], s);
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                kv[t] = bload4s(rs, k_lane + 16u * t, kn);
+            __builtin_amdgcn_sched_barrier(0);
+
             if (j == qb)
             {
                 // diagonal block: key row(r) > query n is masked out (this also
@@ -139,6 +156,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(3))) vo
             m = mn;
             o0 *= corr;
             o1 *= corr;
+            __builtin_amdgcn_sched_barrier(0);
 
             // O^T += V^T P^T: step st contracts key 32j + row(st, hf) for this
             // half, which is exactly the key of accumulator register st
@@ -148,6 +166,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(3))) vo
                 o0 = mfma32(vv[st].x, s[st], o0);
                 o1 = mfma32(vv[st].y, s[st], o1);
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int st = 0; st < 16; ++st)
+                vv[st] = bload2s(rs, v_lane, kn + (uint32_t)(8 * (st >> 2) + (st & 3)) * Wb);
+            __builtin_amdgcn_sched_barrier(0);
         }
 
         if constexpr (NW > 1)
