@@ -23,7 +23,7 @@
 //                          and the dS tile is stored to a workspace. The NW
 //                          partial dK, dV are summed through LDS in a fixed
 //                          order and written once with plain stores.
-//   bwd_dq_d64_kernel      one wave per (b, h, query block i):
+//   bwd_dq_d64_kernel      one wave per (b, h, heavy/light query-block pair):
 //                          dQ_i = sum_{j<=i} dS_ij K_j from the workspace,
 //                          written once with plain stores.
 // Materialising dS costs 4 KiB of workspace per unit (28 MiB per layer at
@@ -402,104 +402,121 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     }
 }
 
-// dQ_i = scale * sum_{j<=i} dS_ij K_j. One workgroup per (b, h, query-block
-// pair (n - 1 - p, p)), n + 1 units; per query block the 4 waves split its key
-// blocks round-robin (rotated per workgroup) and their partial dQ are summed
-// through LDS in a fixed order; wave 0 stores.
-__global__ __launch_bounds__(256) void bwd_dq_d64_kernel(float *__restrict__ grad_x,
+// dQ_i = scale * sum_{j<=i} dS_ij K_j. One WAVE per (b, h, query-block pair
+// (n - 1 - p, p)): n + 1 units, run as one stream (the heavy block's key
+// blocks 0..n-1-p, then the light block's 0..p), so no wave ever waits for
+// another and nothing is merged. A unit's operands (the dS tile and the K
+// block, 12 KiB) are loaded one unit ahead into a second register set while
+// the current unit's 32 MFMAs run. Workgroups hold 4 waves = 4 pairs of one
+// (b, h), ordered (chunk of pairs)-major with (b, h) fastest, the same
+// (b, h) -> XCD mapping as the dK/dV kernel, so a (b, h)'s dS tiles are read
+// from the L2 they were written to.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void bwd_dq_d64_kernel(float *__restrict__ grad_x,
                                                          const float *__restrict__ dsw,
                                                          const float *__restrict__ qkv,
                                                          int T, int C, int H, int bh0, int BHc, int n_qb,
                                                          float scale)
 {
-    constexpr int NW = 4;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int n = lane & 31, hf = lane >> 5;
-    const int pr = (int)(blockIdx.x / BHc);
+    const int chunk = (int)(blockIdx.x / BHc);
     const int bhl = (int)(blockIdx.x % BHc), bh = bh0 + bhl;
     const int b = bh / H, h = bh % H;
+    const int pr = 4 * chunk + w;  // this wave's pair
+    const int n_pairs = (n_qb + 1) / 2;
+    if (pr >= n_pairs)
+        return;
+    const int qa = n_qb - 1 - pr;
+    const bool two = qa != pr;
     const uint32_t Wb = 12u * (uint32_t)C;
     const rsrc_t rk = make_rsrc(qkv + (long)b * T * 3L * C + C + (long)h * 64,
                                 (uint32_t)(((long)T * 3 * C - C - (long)h * 64) * 4));
-    const float *ws = dsw + (long)bhl * ((long)n_qb * (n_qb + 1) / 2) * 1024;
+    const long tiles = (long)n_qb * (n_qb + 1) / 2;
+    const rsrc_t rw = make_rsrc(dsw + (long)bhl * tiles * 1024, (uint32_t)(tiles * 4096));
     float *gx = grad_x + (long)b * T * 3L * C + (long)h * 64;
-    __shared__ float red[2][32][64];
+    // lane parts of the offsets: dS[n][16 hf ..] of a tile, K[16 hf + t][2n ..] of a block
+    const uint32_t w_lane = (uint32_t)n * 128u + 64u * hf;
+    const uint32_t k_lane = 16u * hf * Wb + 8u * (uint32_t)n;
 
-    for (int it = 0; it < 2; ++it)
-    {
-        const int i = it == 0 ? n_qb - 1 - pr : pr;
-        if (it == 1 && i == n_qb - 1 - pr)
-            break;
-        const int rot = (pr + (it == 0 ? 0 : n_qb - pr)) % NW;
-        const int j0 = (w - rot + NW) % NW;
+    // unit u of the stream: query block i(u), key block j(u)
+    const int cnt0 = qa + 1, total = cnt0 + (two ? pr + 1 : 0);
+    auto tile_off = [&](int u) -> uint32_t {
+        if (u >= total)
+            return kNoBlock;
+        const int i = u < cnt0 ? qa : pr, j = u < cnt0 ? u : u - cnt0;
+        return (uint32_t)(((long)i * (i + 1) / 2 + j) * 4096);
+    };
+    auto key_off = [&](int u) -> uint32_t {
+        if (u >= total)
+            return kNoBlock;
+        return 32u * (uint32_t)(u < cnt0 ? u : u - cnt0) * Wb;
+    };
 
-        // dQ[q][d] += dS[q][key] K[key][d]: step t of half hf contracts key
-        // 16 hf + t of the block. A operand dS[n][16 hf + t] (16 contiguous
-        // floats of the tile row), B operand K[key][2n, 2n + 1].
-        v16f a0 = zero16(), a1 = zero16();
-        for (int j = j0; j <= i; j += NW)
+    // Two operand sets, A and B: unit u uses set u % 2; the next unit's set
+    // is loaded while this unit's MFMAs run. (Deeper prefetch does not pay at
+    // B=16, T=256: the kernel is bound by the dS / K reads, not by latency.)
+    float4 dsA[4], dsB[4];   // A operand dS[n][16 hf + t], t = 0..15
+    float2 kkA[16], kkB[16]; // B operand K[32j + 16 hf + t][2n, 2n + 1]
+#define DQ_LOAD(DS, KK, u)                                                        \
+    do                                                                            \
+    {                                                                             \
+        const uint32_t to_ = tile_off(u), ko_ = key_off(u);                       \
+        _Pragma("unroll") for (int e = 0; e < 4; ++e) DS[e] = bload4s(rw, w_lane + 16u * e, to_); \
+        _Pragma("unroll") for (int t = 0; t < 16; ++t) KK[t] = bload2s(rk, k_lane, ko_ + (uint32_t)t * Wb); \
+    } while (0)
+#define DQ_MFMA(DS, KK)                                                           \
+    do                                                                            \
+    {                                                                             \
+        _Pragma("unroll") for (int e = 0; e < 4; ++e)                             \
+        {                                                                         \
+            a0 = mfma32(DS[e].x, KK[4 * e + 0].x, a0);                            \
+            a1 = mfma32(DS[e].x, KK[4 * e + 0].y, a1);                            \
+            a0 = mfma32(DS[e].y, KK[4 * e + 1].x, a0);                            \
+            a1 = mfma32(DS[e].y, KK[4 * e + 1].y, a1);                            \
+            a0 = mfma32(DS[e].z, KK[4 * e + 2].x, a0);                            \
+            a1 = mfma32(DS[e].z, KK[4 * e + 2].y, a1);                            \
+            a0 = mfma32(DS[e].w, KK[4 * e + 3].x, a0);                            \
+            a1 = mfma32(DS[e].w, KK[4 * e + 3].y, a1);                            \
+        }                                                                         \
+    } while (0)
+    v16f a0 = zero16(), a1 = zero16();
+    // last unit of a query block: register r of lane (n, hf) holds
+    // dQ[32 i + row(r, hf)][2n, 2n + 1]
+    auto flush = [&](int u) {
+        if (u == cnt0 - 1 || u == total - 1)
         {
-            const float4 *tile = reinterpret_cast<const float4 *>(ws + ds_tile(i, j) + n * 32 + 16 * hf);
-            float4 d4[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                d4[u] = tile[u];
-            const float dsr[16] = {d4[0].x, d4[0].y, d4[0].z, d4[0].w, d4[1].x, d4[1].y, d4[1].z, d4[1].w,
-                                   d4[2].x, d4[2].y, d4[2].z, d4[2].w, d4[3].x, d4[3].y, d4[3].z, d4[3].w};
-            const uint32_t kb = (uint32_t)(32 * j + 16 * hf) * Wb + 8u * n;
-#pragma unroll
-            for (int t = 0; t < 16; ++t)
-            {
-                const float2 k2 = bload2(rk, kb + (uint32_t)t * Wb);
-                a0 = mfma32(dsr[t], k2.x, a0);
-                a1 = mfma32(dsr[t], k2.y, a1);
-            }
-        }
-        // (w0 + w1) + (w2 + w3)
-        if (w & 1)
-        {
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-            {
-                red[w >> 1][r][lane] = a0[r];
-                red[w >> 1][16 + r][lane] = a1[r];
-            }
-        }
-        __syncthreads();
-        if (!(w & 1))
-        {
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-            {
-                a0[r] += red[w >> 1][r][lane];
-                a1[r] += red[w >> 1][16 + r][lane];
-            }
-        }
-        __syncthreads();
-        if (w == 2)
-        {
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-            {
-                red[0][r][lane] = a0[r];
-                red[0][16 + r][lane] = a1[r];
-            }
-        }
-        __syncthreads();
-        if (w == 0)
-        {
-            // register r of lane (n, hf): dQ[32 i + row(r, hf)][2n, 2n + 1]
+            const int i = u < cnt0 ? qa : pr;
 #pragma unroll
             for (int r = 0; r < 16; ++r)
             {
                 const int row = 32 * i + mfma_row(r, hf);
                 if (row < T)
                     *reinterpret_cast<float2 *>(gx + (long)row * 3 * C + 2 * n) =
-                        make_float2((a0[r] + red[0][r][lane]) * scale, (a1[r] + red[0][16 + r][lane]) * scale);
+                        make_float2(a0[r] * scale, a1[r] * scale);
             }
+            a0 = zero16();
+            a1 = zero16();
         }
-        __syncthreads();  // red is reused by the next query block
+    };
+
+    DQ_LOAD(dsA, kkA, 0);
+    for (int u = 0; u < total; u += 2)
+    {
+        DQ_LOAD(dsB, kkB, u + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        DQ_MFMA(dsA, kkA);
+        __builtin_amdgcn_sched_barrier(0);
+        flush(u);
+        if (u + 1 >= total)
+            break;
+        DQ_LOAD(dsA, kkA, u + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        DQ_MFMA(dsB, kkB);
+        __builtin_amdgcn_sched_barrier(0);
+        flush(u + 1);
     }
+#undef DQ_LOAD
+#undef DQ_MFMA
 }
 
 // General head_dim: dQ rows, one thread per (b, h, query i), keys j <= i.
@@ -666,9 +683,10 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
         hipLaunchKernelGGL(bwd_dkdv_d64_kernel, dim3(blocks), dim3(256), 0, st, grad_x, ws, lse, D, dy, qkv, s.T,
                            s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale);
         timer_end(st);
+        const unsigned dq_blocks = (unsigned)((long)((n_qb + 1) / 2 + 3) / 4 * cnt);  // 4 pairs per workgroup
         timer_begin(kKindDq, st);
-        hipLaunchKernelGGL(bwd_dq_d64_kernel, dim3(blocks), dim3(256), 0, st, grad_x, ws, qkv, s.T, s.C, s.H, bh0,
-                           cnt, n_qb, scale);
+        hipLaunchKernelGGL(bwd_dq_d64_kernel, dim3(dq_blocks), dim3(256), 0, st, grad_x, ws, qkv, s.T, s.C, s.H,
+                           bh0, cnt, n_qb, scale);
         timer_end(st);
         e = hipGetLastError();
         if (e != hipSuccess)
