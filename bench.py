@@ -27,6 +27,8 @@ Also reported:
 
 Usage:
   python bench.py [--gpus 1] [--steps K] [--warmup W]       the metric line
+  python bench.py --no-cpu --bwd-path 2                     same workload with the fp32-atomic
+                                                            dQ backward (for profiling)
   python bench.py --copy-calibration                        256 MiB device copy x5
                                                             (run under --pmc)
   python bench.py --traffic KERNEL FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
@@ -119,6 +121,9 @@ def parse():
     ap.add_argument("--cpu-layers", type=int, default=12,
                     help="layers of the workload timed on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--bwd-path", type=int, default=0, choices=(0, 2),
+                    help="backward variant for profiling: 0 deterministic dS-tile dQ (default), "
+                         "2 fp32-atomic dQ (gpt_hip_attn_set_path)")
     return ap.parse_args()
 
 
@@ -174,6 +179,8 @@ def main():
 
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
+    if args.bwd_path:
+        gpt_amd.set_path(args.bwd_path)
     scales = synth.layer_scales(LAYERS, CONFIG_SEED)
 
     # Per-layer buffers, as GPT::set_size lays them out (gpt.cpp:101-214).
@@ -274,6 +281,7 @@ def main():
             "workload": "GPT-2 124M attention micro-step: 12 layers x causal fwd+bwd, B=16 T=256 H=12 d=64",
             "layers": LAYERS, "batch": B, "seq_len": T, "heads": H, "head_dim": D_HEAD,
             "flops_per_step": step_flops,
+            **({"bwd_path": args.bwd_path} if args.bwd_path else {}),
         },
         "pct_fp32_mfma_peak": round(100 * tflops / PEAK_FP32_MFMA_TFLOPS, 2),
         "fwd": {"avg_ms": round(fwd_avg_ms, 5), "tflops": round(fwd_tf, 3)},
