@@ -29,6 +29,10 @@ Usage:
   python bench.py [--gpus 1] [--steps K] [--warmup W]       the metric line
   python bench.py --no-cpu --bwd-path 2                     same workload with the fp32-atomic
                                                             dQ backward (for profiling)
+  python bench.py --prefix-sweep [--no-cpu]                 BASELINE config 5(b): forward at B=1
+                                                            for every prefix T=1..256 (the reference's
+                                                            generation loop without a KV cache); one
+                                                            JSON line of its own
   python bench.py --copy-calibration                        256 MiB device copy x5
                                                             (run under --pmc)
   python bench.py --traffic KERNEL FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
@@ -121,6 +125,8 @@ def parse():
     ap.add_argument("--cpu-layers", type=int, default=12,
                     help="layers of the workload timed on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--prefix-sweep", action="store_true",
+                    help="time BASELINE config 5(b) (forward, B=1, T=1..256) instead of the headline")
     ap.add_argument("--bwd-path", type=int, default=0, choices=(0, 2),
                     help="backward variant for profiling: 0 deterministic dS-tile dQ (default), "
                          "2 fp32-atomic dQ (gpt_hip_attn_set_path)")
@@ -158,6 +164,84 @@ def cpu_baseline(layers: int):
     }
 
 
+PREFIX_SEED = 1239  # 1234 + config index 5
+
+
+def prefix_sweep(args):
+    """BASELINE config 5(b): y, lse for qkv[:, :T] at B=1, every T in 1..256,
+    each prefix its own contiguous [1, T, 3C] tensor (the reference's inference
+    loop re-sizes its activations every token, infer.cpp:117, gpt.cpp:399-424).
+    value = total forward FLOPs of the sweep / summed GPU time, where each T's
+    time is the median of `reps` event-timed calls on resident inputs (each rep
+    is queued behind a GPU spin, so the host's launch latency is not timed)."""
+    import numpy as np
+    import torch
+
+    import gpt_amd
+    from gpt_amd import synth
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    Tmax, reps = 256, 7
+    x = synth.qkv(1, Tmax, C, PREFIX_SEED)
+    xs = [torch.from_numpy(np.ascontiguousarray(x[:, :t])).to(dev) for t in range(1, Tmax + 1)]
+    ys = [torch.empty(1, t, C, device=dev) for t in range(1, Tmax + 1)]
+    ls = [torch.empty(1, t, H, device=dev) for t in range(1, Tmax + 1)]
+    for t in range(1, Tmax + 1):  # warm every shape once
+        gpt_amd.device_flash_attention_forward(ys[t - 1], ls[t - 1], xs[t - 1], 1, t, C, H, stream)
+    torch.cuda.synchronize()
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+          for _ in range(Tmax)]
+    for r in range(reps):
+        # queue the rep behind a ~10 ms GPU spin, so the events time the GPU
+        # only, not the host's per-call launch latency
+        torch.cuda._sleep(20_000_000)
+        for t in range(1, Tmax + 1):
+            e0, e1 = ev[t - 1][r]
+            e0.record(stream)
+            gpt_amd.device_flash_attention_forward(ys[t - 1], ls[t - 1], xs[t - 1], 1, t, C, H, stream)
+            e1.record(stream)
+    # the same timing around a one-element fill kernel: the per-call floor of
+    # this method (event packets, dispatch, kernel start-up) on this GPU
+    tiny = torch.empty(1, device=dev)
+    fl = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(64)]
+    torch.cuda._sleep(20_000_000)
+    for e0, e1 in fl:
+        e0.record(stream)
+        tiny.fill_(1.0)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    per_t_us = [float(np.median([a.elapsed_time(b) for a, b in ev[t]])) * 1e3 for t in range(Tmax)]
+    floor_us = float(np.median([a.elapsed_time(b) for a, b in fl])) * 1e3
+    total_us = sum(per_t_us)
+    flops = sum(attn_flops(1, t, H, D_HEAD, bwd=False) for t in range(1, Tmax + 1))
+    out = {
+        "metric": "causal attn forward prefix sweep TFLOP/s, B=1 T=1..256 (generation without KV cache), 1 GPU",
+        "value": round(flops / (total_us * 1e-6) / 1e12, 4),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "higher_is_better": True,
+        "dtype": "fp32",
+        "data": "synthetic (splitmix64 Box-Muller; Q/K/V ~ N(0,1))",
+        "config": {"workload": "BASELINE config 5(b): forward, B=1, every prefix T=1..256, H=12 d=64",
+                   "flops": flops, "reps_per_T": reps},
+        "sweep_ms": round(total_us / 1e3, 4),
+        "us_at_T": {str(t): round(per_t_us[t - 1], 2) for t in (1, 2, 32, 33, 64, 128, 200, 256)},
+        "fill_kernel_floor_us": round(floor_us, 2),
+    }
+    if not args.no_cpu:
+        from oracle import pyoracle
+
+        impl, kind = ("ref_fast", "reference") if pyoracle.ref_available(fast=True) else ("oracle", "port")
+        t0 = time.perf_counter()
+        for t in range(1, Tmax + 1):
+            pyoracle.forward(np.ascontiguousarray(x[:, :t]), H, impl)
+        cpu_s = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(flops / cpu_s / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": kind,
+                               "sample": f"the whole sweep, {cpu_s:.2f} s on 1 thread"}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.traffic:
@@ -170,6 +254,9 @@ def main():
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the attention op "
               f"shards per (batch, head) with no communication; run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.prefix_sweep:
+        prefix_sweep(args)
+        return
 
     import numpy as np
     import torch

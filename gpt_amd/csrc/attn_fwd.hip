@@ -11,8 +11,8 @@
 // 32-key block of the causal triangle; query block i has i + 1 units. Each
 // workgroup takes a heavy/light pair of query blocks (n - 1 - p, p) of one
 // (b, h), i.e. n + 1 units for n query blocks, so every workgroup carries the
-// same work. Its NW waves (4 for small problems, else 2) split each query
-// block's key blocks round-robin; the rotation of the second block is chosen
+// same work. Its NW waves (2 for large problems, 4 for small ones, 1 for a
+// single query block) split each query block's key blocks round-robin; the rotation of the second block is chosen
 // so its spare units go to the waves that got none in the first, which bounds
 // every wave at ceil((n + 1) / NW) units. Each wave runs its units of both query blocks as ONE software-
 // pipelined stream: while a unit's softmax and PV run, the next unit's K (and,
@@ -396,15 +396,28 @@ hipError_t launch_fwd_d64(float *y, float *lse, const float *qkv, const Shape &s
     const long blocks = (long)((n_qb + 1) / 2) * BH;  // heavy/light pairs
     const float c2 = softmax_scale(64) * kLog2e;
     // Waves per pair: 4 while the pairs alone leave most of the 1024 SIMDs
-    // idle, else 2 (fewer, longer streams and one partial to merge per block;
-    // measured equal at B=16 T=256 and 5-15 % faster at T >= 1024 or B = 64).
+    // idle, else 2 (fewer, longer streams, one partial to merge per block;
+    // equal at B=16 T=256, 5-15 % faster at T >= 1024 or B = 64); never more
+    // waves than the pair has units (one query block: no merge at all).
+    int nw = blocks > 256 ? 2 : 4;
+    while (nw > 1 && nw > n_qb + 1)
+        nw >>= 1;
+    if (n_qb == 1)
+        nw = 1;
     timer_begin(kKindFwd, st);
-    if (blocks <= 256)
-        hipLaunchKernelGGL(fwd_d64_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, st, y, lse, qkv, s.T, s.C, s.H,
-                           BH, n_qb, c2);
-    else
-        hipLaunchKernelGGL(fwd_d64_kernel<2>, dim3((unsigned)blocks), dim3(128), 0, st, y, lse, qkv, s.T, s.C, s.H,
-                           BH, n_qb, c2);
+    const dim3 grid((unsigned)blocks);
+    switch (nw)
+    {
+    case 4:
+        hipLaunchKernelGGL(fwd_d64_kernel<4>, grid, dim3(256), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_qb, c2);
+        break;
+    case 2:
+        hipLaunchKernelGGL(fwd_d64_kernel<2>, grid, dim3(128), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_qb, c2);
+        break;
+    default:
+        hipLaunchKernelGGL(fwd_d64_kernel<1>, grid, dim3(64), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_qb, c2);
+        break;
+    }
     timer_end(st);
     return hipGetLastError();
 }
