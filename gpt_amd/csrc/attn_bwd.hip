@@ -122,92 +122,51 @@ __global__ __launch_bounds__(256) void bwd_rowdot_d64_kernel(float *__restrict__
 // Offset (floats) of dS tile (i, j), j <= i, inside one (b, h)'s workspace.
 __device__ __forceinline__ long ds_tile(int i, int j) { return ((long)i * (i + 1) / 2 + j) * 1024; }
 
-// Sum one 64-register-per-lane partial (v0..v3, 16 registers each) over the
-// NW = 4 waves of the workgroup in the fixed order (w0 + w1) + (w2 + w3);
-// wave 0 ends with the total. `red` holds two [64][64] partials.
-__device__ __forceinline__ void reduce4(v16f &v0, v16f &v1, v16f &v2, v16f &v3, float (*red)[64][64], int w,
-                                        int lane)
-{
-    if (w & 1)
-    {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-        {
-            red[w >> 1][r][lane] = v0[r];
-            red[w >> 1][16 + r][lane] = v1[r];
-            red[w >> 1][32 + r][lane] = v2[r];
-            red[w >> 1][48 + r][lane] = v3[r];
-        }
-    }
-    __syncthreads();
-    if (!(w & 1))
-    {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-        {
-            v0[r] += red[w >> 1][r][lane];
-            v1[r] += red[w >> 1][16 + r][lane];
-            v2[r] += red[w >> 1][32 + r][lane];
-            v3[r] += red[w >> 1][48 + r][lane];
-        }
-    }
-    __syncthreads();
-    if (w == 2)
-    {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-        {
-            red[0][r][lane] = v0[r];
-            red[0][16 + r][lane] = v1[r];
-            red[0][32 + r][lane] = v2[r];
-            red[0][48 + r][lane] = v3[r];
-        }
-    }
-    __syncthreads();
-    if (w == 0)
-    {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-        {
-            v0[r] += red[0][r][lane];
-            v1[r] += red[0][16 + r][lane];
-            v2[r] += red[0][32 + r][lane];
-            v3[r] += red[0][48 + r][lane];
-        }
-    }
-}
-
-// dK, dV and the dS tiles. One workgroup per (b, h, key-block pair
-// (p, n - 1 - p)): key block j has n - j units (query blocks j .. n - 1), so
-// each pair carries n + 1 units. The pair's two key blocks are done one after
-// the other; for each, K and V are staged once in LDS (row stride
-// kRowStride) and the 4 waves split its query blocks round-robin (rotated per
-// workgroup), accumulating partial dK / dV in registers that are summed
-// through LDS in a fixed order and stored by wave 0.
-//
-// Per unit (query block i) a wave runs two MFMA phases:
-//   phase 1  S = Q K^T, dP = dO V^T: 8 chunks of 4 + 4 MFMAs; A operands
-//            Q / dO[q0 + n][32 hf + 4c ..] (one float4 each per chunk, from
-//            L2), B operands K / V from LDS
-//   phase 2  dV += P^T dO, dK += dS^T Q: 8 chunks of 2 steps x 4 MFMAs; B
-//            operands dO / Q[q0 + row(st, hf)][2n, 2n + 1] (float2, from L2)
-// Every global operand is loaded one chunk ahead, and the first chunk of each
-// phase one phase ahead: phase 2's while P and dS are formed, the next unit's
-// phase 1 (and its lse / D rows) during this unit's phase 2. All row and block
-// offsets are wave-uniform and go in the buffer loads' scalar offset; rows past
-// T read as zeros through the buffer range check. 3 waves per SIMD keep all
-// workgroups of a B=16, T=256, H=12 call resident at once.
+// dK, dV and the dS tiles, K/V-stationary. One workgroup per (b, h, 64-key
+// group J); wave w owns the 16 keys kw0 = 64 J + 16 w .. kw0 + 15: their K and
+// V rows stay in registers as MFMA B operands and their dK, dV accumulate in
+// registers, so no wave shares an output with another and nothing is reduced.
+// The 4 waves walk the query blocks i = 2J .. n - 1 together; each block's Q,
+// dO (32 x 64) and lse, D rows are staged once in LDS for all 4 waves (double
+// buffered: block i + 1 is loaded into registers while block i is computed,
+// then written to the other buffer; one barrier per block). Per wave and query
+// block, on v_mfma_f32_16x16x4_f32 (two 16-row query halves t):
+//   S_t = Q_t K^T, dP_t = dO_t V^T          (16 queries x 16 keys, 16 MFMAs each)
+//   P = 2^(S c - L), dS = P (dP - D)        (masked past the diagonal and T)
+//   dV += P^T dO, dK += dS^T Q              (S / dP accumulators are the A
+//                                            operands as they are; 4 d-tiles)
+// and the wave's 32 x 16 half of dS tile (i, kw0 / 32) is stored. Workgroups
+// are ordered key-group-major (heaviest first), (b, h) fastest.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void bwd_dkdv_d64_kernel(
     float *__restrict__ grad_x, float *__restrict__ dsw, const float *__restrict__ lse,
     const float *__restrict__ Dv, const float *__restrict__ dy, const float *__restrict__ qkv, int T, int C, int H,
-    int bh0, int BHc, int n_qb, float c2, float scale)
+    int bh0, int BHc, int n_qb, float c2, float scale, int n_cu)
 {
-    constexpr int NW = 4, ST = kRowStride;
+    constexpr int ST = kRowStride;
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
-    const int n = lane & 31, hf = lane >> 5;
-    const int pr = (int)(blockIdx.x / BHc);
-    const int bhl = (int)(blockIdx.x % BHc), bh = bh0 + bhl;
+    const int c16 = lane & 15, g4 = lane >> 4;
+    // Work item = (key group J, (b, h)), heaviest first: J-major, (b, h)
+    // fastest. When the whole grid is resident (at most 3 workgroups per CU),
+    // workgroup c, c + n_cu and c + 2 n_cu share a CU (round-robin dispatch),
+    // so the middle round takes the items in reverse order (in blocks of 8,
+    // which keeps every (b, h) on one XCD): each CU then gets one heavy, one
+    // light and one middle item instead of three of a kind.
+    int item = (int)blockIdx.x;
+    {
+        const int G = (int)gridDim.x;
+        if (n_cu > 0 && n_cu % 8 == 0 && G % n_cu == 0 && G / n_cu <= 3)
+        {
+            const int r = item / n_cu;
+            int c = item % n_cu;
+            if (r & 1)
+                c = (n_cu / 8 - 1 - c / 8) * 8 + (c & 7);
+            item = r * n_cu + c;
+        }
+    }
+    const int J = item / BHc;
+    const int bhl = item % BHc, bh = bh0 + bhl;
     const int b = bh / H, h = bh % H;
+    const int kw0 = 64 * J + 16 * w;
     const uint32_t Wb = 12u * (uint32_t)C, Cb = 4u * (uint32_t)C, Hb = 4u * (uint32_t)H;
     const rsrc_t rq = make_rsrc(qkv + (long)b * T * 3L * C + (long)h * 64,
                                 (uint32_t)(((long)T * 3 * C - (long)h * 64) * 4));
@@ -217,187 +176,172 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     float *ws = dsw + (long)bhl * ((long)n_qb * (n_qb + 1) / 2) * 1024;
     float *gx = grad_x + (long)b * T * 3L * C + (long)h * 64;
 
-    // lane-dependent parts of the operand offsets (bytes)
-    const uint32_t q1_lane = (uint32_t)n * Wb + 128u * hf;      // phase 1: Q[n][32 hf ..]
-    const uint32_t o1_lane = (uint32_t)n * Cb + 128u * hf;      // phase 1: dO[n][32 hf ..]
-    const uint32_t q2_lane = 4u * hf * Wb + 8u * (uint32_t)n;   // phase 2: Q[4 hf + ..][2n ..]
-    const uint32_t o2_lane = 4u * hf * Cb + 8u * (uint32_t)n;   // phase 2: dO[4 hf + ..][2n ..]
-    const uint32_t l_lane = (uint32_t)n * Hb;                    // lse / D row n
+    __shared__ __attribute__((aligned(16))) float sq[2][32 * ST], so[2][32 * ST];  // Q, dO of the block
+    __shared__ __attribute__((aligned(16))) float sl[2][32], sd[2][32];             // lse * log2(e), D
 
-    __shared__ __attribute__((aligned(16))) float kv_lds[2][32 * ST];  // K, V of the key block
-    __shared__ __attribute__((aligned(16))) float ld_lds[NW][2][32];   // per wave: L * log2(e), D
-    __shared__ float red[2][64][64];
-
-    for (int it = 0; it < 2; ++it)
+    // stationary B operands: lane l holds K / V[kw0 + l%16][16 (l/16) + m],
+    // m = 0..15 (MFMA m contracts d = m + 16 kk, kk = l/16)
+    float kreg[16], vreg[16];
     {
-        const int j = it == 0 ? pr : n_qb - 1 - pr;
-        if (it == 1 && j == pr)
-            break;  // odd n_qb: the middle key block has no partner
-        const int k0 = 32 * j;
-        // wave w takes query blocks i = j + u with (u + rot) % NW == w
-        const int rot = (pr + (it == 0 ? 0 : n_qb - pr)) % NW;
-        const int i_first = j + (w - rot + NW) % NW;
-
-        // first unit's phase-1 chunk 0 and lse / D rows, in flight while K / V
-        // are staged
-        float4 qa[2], oa[2];
-        float lrow, drow;
-        {
-            const uint32_t rq0 = i_first < n_qb ? 32u * (uint32_t)i_first * Wb : kNoBlock;
-            const uint32_t ro0 = i_first < n_qb ? 32u * (uint32_t)i_first * Cb : kNoBlock;
-            const uint32_t rl0 = i_first < n_qb ? 32u * (uint32_t)i_first * Hb : kNoBlock;
-            qa[0] = bload4s(rq, q1_lane, rq0);
-            oa[0] = bload4s(ro, o1_lane, ro0);
-            lrow = bload1s(rl, l_lane, rl0);
-            drow = bload1s(rd, l_lane, rl0);
-        }
-
-        __syncthreads();  // the previous key block's LDS reads are done
+        const uint32_t off = (uint32_t)c16 * Wb + 64u * g4;
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int c = 0; c < 4; ++c)
         {
-            const int idx = tid + 256 * u, which = idx >> 9, r = (idx >> 4) & 31, c4 = idx & 15;
-            const float4 v = bload4s(rq, (uint32_t)r * Wb + (1u + which) * Cb + 16u * c4, (uint32_t)k0 * Wb);
-            *reinterpret_cast<float4 *>(&kv_lds[which][r * ST + 4 * c4]) = v;
+            const float4 k4 = bload4s(rq, off + Cb + 16u * c, (uint32_t)kw0 * Wb);
+            const float4 v4 = bload4s(rq, off + 2u * Cb + 16u * c, (uint32_t)kw0 * Wb);
+            kreg[4 * c + 0] = k4.x;
+            kreg[4 * c + 1] = k4.y;
+            kreg[4 * c + 2] = k4.z;
+            kreg[4 * c + 3] = k4.w;
+            vreg[4 * c + 0] = v4.x;
+            vreg[4 * c + 1] = v4.y;
+            vreg[4 * c + 2] = v4.z;
+            vreg[4 * c + 3] = v4.w;
         }
-        __syncthreads();
+    }
 
-        const float *kr = &kv_lds[0][n * ST + 32 * hf];
-        const float *vr = &kv_lds[1][n * ST + 32 * hf];
-        v16f dk0 = zero16(), dk1 = zero16(), dv0 = zero16(), dv1 = zero16();
-        for (int i = i_first; i < n_qb; i += NW)
-        {
-            const int q0 = 32 * i;
-            const bool more = i + NW < n_qb;
-            const uint32_t rqn = more ? 32u * (uint32_t)(i + NW) * Wb : kNoBlock;
-            const uint32_t ron = more ? 32u * (uint32_t)(i + NW) * Cb : kNoBlock;
-            const uint32_t rln = more ? 32u * (uint32_t)(i + NW) * Hb : kNoBlock;
-            if (hf == 0)
-            {
-                ld_lds[w][0][n] = lrow * kLog2e;
-                ld_lds[w][1][n] = drow;
-            }
-
-            // phase 1: S[query q0 + row(r)][key k0 + n], dP likewise
-            v16f s = zero16(), dp = zero16();
+    // staging: thread tid moves float4s tid + 256 u (u = 0, 1) of the Q and dO
+    // tiles (row = idx / 16, column 4 (idx % 16)); threads 0..31 an lse row,
+    // 32..63 a D row
+    constexpr int NT = 256, NU = 512 / NT;
+    const int r0 = tid >> 4, cc = tid & 15;
+    const uint32_t st_q = (uint32_t)r0 * Wb + 16u * cc, st_o = (uint32_t)r0 * Cb + 16u * cc;
+    float4 pq[NU], po[NU];
+    float pld = 0.f;
+    auto issue = [&](int i) {
+        const bool ok = i < n_qb;
+        const uint32_t qo = ok ? 32u * (uint32_t)i * Wb : kNoBlock, oo = ok ? 32u * (uint32_t)i * Cb : kNoBlock;
 #pragma unroll
-            for (int c = 0; c < 8; ++c)
+        for (int u = 0; u < NU; ++u)
+        {
+            pq[u] = bload4s(rq, st_q + (uint32_t)(u * NT / 16) * Wb, qo);
+            po[u] = bload4s(ro, st_o + (uint32_t)(u * NT / 16) * Cb, oo);
+        }
+        const uint32_t lo = ok ? 32u * (uint32_t)i * Hb : kNoBlock;
+        if (tid < 32)
+            pld = bload1s(rl, (uint32_t)tid * Hb, lo) * kLog2e;
+        else if (tid < 64)
+            pld = bload1s(rd, (uint32_t)(tid - 32) * Hb, lo);
+    };
+    auto commit = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+        {
+            *reinterpret_cast<float4 *>(&sq[buf][(r0 + u * NT / 16) * ST + 4 * cc]) = pq[u];
+            *reinterpret_cast<float4 *>(&so[buf][(r0 + u * NT / 16) * ST + 4 * cc]) = po[u];
+        }
+        if (tid < 32)
+            sl[buf][tid] = pld;
+        else if (tid < 64)
+            sd[buf][tid - 32] = pld;
+    };
+
+    v4f dk0 = zero4(), dk1 = zero4(), dk2 = zero4(), dk3 = zero4();
+    v4f dv0 = zero4(), dv1 = zero4(), dv2 = zero4(), dv3 = zero4();
+    const int i_lo = 2 * J;
+    issue(i_lo);
+    commit(0);
+    __syncthreads();
+    for (int i = i_lo; i < n_qb; ++i)
+    {
+        const int buf = (i - i_lo) & 1;
+        issue(i + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        const int q0 = 32 * i;
+        if (kw0 <= q0 + 31)  // else all 16 keys lie past this block's last query: no tile
+        {
+            const float *Qs = sq[buf], *Os = so[buf];
+            // S_t[query q0 + 16t + 4 g4 + r][key kw0 + c16], dP likewise
+            v4f s0 = zero4(), s1 = zero4(), p0 = zero4(), p1 = zero4();
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
             {
-                if (c < 7)
+                const float4 qa0 = *reinterpret_cast<const float4 *>(Qs + c16 * ST + 16 * g4 + 4 * c);
+                const float4 qa1 = *reinterpret_cast<const float4 *>(Qs + (16 + c16) * ST + 16 * g4 + 4 * c);
+                const float4 oa0 = *reinterpret_cast<const float4 *>(Os + c16 * ST + 16 * g4 + 4 * c);
+                const float4 oa1 = *reinterpret_cast<const float4 *>(Os + (16 + c16) * ST + 16 * g4 + 4 * c);
+                const float q0v[4] = {qa0.x, qa0.y, qa0.z, qa0.w}, q1v[4] = {qa1.x, qa1.y, qa1.z, qa1.w};
+                const float o0v[4] = {oa0.x, oa0.y, oa0.z, oa0.w}, o1v[4] = {oa1.x, oa1.y, oa1.z, oa1.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
                 {
-                    qa[(c + 1) & 1] = bload4s(rq, q1_lane + 16u * (c + 1), (uint32_t)q0 * Wb);
-                    oa[(c + 1) & 1] = bload4s(ro, o1_lane + 16u * (c + 1), (uint32_t)q0 * Cb);
+                    s0 = mfma16(q0v[e], kreg[4 * c + e], s0);
+                    s1 = mfma16(q1v[e], kreg[4 * c + e], s1);
+                    p0 = mfma16(o0v[e], vreg[4 * c + e], p0);
+                    p1 = mfma16(o1v[e], vreg[4 * c + e], p1);
                 }
-                __builtin_amdgcn_sched_barrier(0);
-                const float4 q4 = qa[c & 1], o4 = oa[c & 1];
-                const float4 kb = *reinterpret_cast<const float4 *>(kr + 4 * c);
-                const float4 vb = *reinterpret_cast<const float4 *>(vr + 4 * c);
-                s = mfma32(q4.x, kb.x, s);
-                dp = mfma32(o4.x, vb.x, dp);
-                s = mfma32(q4.y, kb.y, s);
-                dp = mfma32(o4.y, vb.y, dp);
-                s = mfma32(q4.z, kb.z, s);
-                dp = mfma32(o4.z, vb.z, dp);
-                s = mfma32(q4.w, kb.w, s);
-                dp = mfma32(o4.w, vb.w, dp);
-                __builtin_amdgcn_sched_barrier(0);
             }
-
-            // phase 2's chunk 0 (query rows 4 hf + {0, 1}), in flight while P and
-            // dS are formed
-            float2 gb[2][2], qb[2][2];
-#pragma unroll
-            for (int e = 0; e < 2; ++e)
-            {
-                gb[0][e] = bload2s(ro, o2_lane, (uint32_t)(q0 + e) * Cb);
-                qb[0][e] = bload2s(rq, q2_lane, (uint32_t)(q0 + e) * Wb);
-            }
-            wave_lds_sync();
-            __builtin_amdgcn_sched_barrier(0);
             // P and dS (without the 1/sqrt(d)); zero where key > query or the
-            // query row is past T.
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
+            // query row is past T
             {
-                const float4 l4 = *reinterpret_cast<const float4 *>(&ld_lds[w][0][8 * g + 4 * hf]);
-                const float4 d4 = *reinterpret_cast<const float4 *>(&ld_lds[w][1][8 * g + 4 * hf]);
-                const float lj[4] = {l4.x, l4.y, l4.z, l4.w};
-                const float dj[4] = {d4.x, d4.y, d4.z, d4.w};
+                const float4 L0 = *reinterpret_cast<const float4 *>(&sl[buf][4 * g4]);
+                const float4 L1 = *reinterpret_cast<const float4 *>(&sl[buf][16 + 4 * g4]);
+                const float4 D0 = *reinterpret_cast<const float4 *>(&sd[buf][4 * g4]);
+                const float4 D1 = *reinterpret_cast<const float4 *>(&sd[buf][16 + 4 * g4]);
+                const float l0v[4] = {L0.x, L0.y, L0.z, L0.w}, l1v[4] = {L1.x, L1.y, L1.z, L1.w};
+                const float d0v[4] = {D0.x, D0.y, D0.z, D0.w}, d1v[4] = {D1.x, D1.y, D1.z, D1.w};
+                const int key = kw0 + c16;
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
+                for (int r = 0; r < 4; ++r)
                 {
-                    const int r = 4 * g + jj;
-                    const int qrow = q0 + 8 * g + 4 * hf + jj;  // = q0 + row(r, hf)
-                    const bool keep = (k0 + n <= qrow) && (qrow < T);
-                    const float p = fast_exp2(s[r] * c2 - lj[jj]);
-                    s[r] = keep ? p : 0.f;
-                    dp[r] = keep ? p * (dp[r] - dj[jj]) : 0.f;
+                    const int qa = q0 + 4 * g4 + r, qb = qa + 16;
+                    const bool ka = key <= qa && qa < T, kb = key <= qb && qb < T;
+                    const float pa = fast_exp2(s0[r] * c2 - l0v[r]), pb = fast_exp2(s1[r] * c2 - l1v[r]);
+                    s0[r] = ka ? pa : 0.f;
+                    p0[r] = ka ? pa * (p0[r] - d0v[r]) : 0.f;
+                    s1[r] = kb ? pb : 0.f;
+                    p1[r] = kb ? pb * (p1[r] - d1v[r]) : 0.f;
                 }
             }
-            // dS tile, query-major (row = query, column = key)
+            // this wave's 32 x 16 half of dS tile (i, kw0 / 32), query-major
             {
-                float *tile = ws + ds_tile(i, j) + (4 * hf) * 32 + n;
+                float *tile = ws + ds_tile(i, kw0 >> 5) + (kw0 & 31) + c16 + (4 * g4) * 32;
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    tile[(8 * (r >> 2) + (r & 3)) * 32] = dp[r];
+                for (int r = 0; r < 4; ++r)
+                {
+                    tile[r * 32] = p0[r];
+                    tile[(16 + r) * 32] = p1[r];
+                }
             }
-            __builtin_amdgcn_sched_barrier(0);
-
-            // phase 2: step st contracts query q0 + row(st, hf), the query of
-            // accumulator register st; chunk c = steps 2c, 2c + 1
+            // dV += P^T dO, dK += dS^T Q: step (t, r) contracts queries
+            // q0 + 16t + 4kk + r (kk = l/16); B operands dO / Q[that query][4 c16 + e]
 #pragma unroll
-            for (int c = 0; c < 8; ++c)
+            for (int t = 0; t < 2; ++t)
             {
-                if (c < 7)
-                {
 #pragma unroll
-                    for (int e = 0; e < 2; ++e)
-                    {
-                        const int st = 2 * (c + 1) + e;
-                        const uint32_t row = (uint32_t)(q0 + 8 * (st >> 2) + (st & 3));
-                        gb[(c + 1) & 1][e] = bload2s(ro, o2_lane, row * Cb);
-                        qb[(c + 1) & 1][e] = bload2s(rq, q2_lane, row * Wb);
-                    }
-                }
-                if (c == 3)
+                for (int r = 0; r < 4; ++r)
                 {
-                    // next unit's phase-1 chunk 0 and lse / D rows
-                    qa[0] = bload4s(rq, q1_lane, rqn);
-                    oa[0] = bload4s(ro, o1_lane, ron);
-                    lrow = bload1s(rl, l_lane, rln);
-                    drow = bload1s(rd, l_lane, rln);
+                    const int row = 16 * t + 4 * g4 + r;
+                    const float4 ob = *reinterpret_cast<const float4 *>(Os + row * ST + 4 * c16);
+                    const float4 qb = *reinterpret_cast<const float4 *>(Qs + row * ST + 4 * c16);
+                    const float ap = t == 0 ? s0[r] : s1[r], ad = t == 0 ? p0[r] : p1[r];
+                    dv0 = mfma16(ap, ob.x, dv0);
+                    dv1 = mfma16(ap, ob.y, dv1);
+                    dv2 = mfma16(ap, ob.z, dv2);
+                    dv3 = mfma16(ap, ob.w, dv3);
+                    dk0 = mfma16(ad, qb.x, dk0);
+                    dk1 = mfma16(ad, qb.y, dk1);
+                    dk2 = mfma16(ad, qb.z, dk2);
+                    dk3 = mfma16(ad, qb.w, dk3);
                 }
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int e = 0; e < 2; ++e)
-                {
-                    const int st = 2 * c + e;
-                    const float2 g2 = gb[c & 1][e], q2 = qb[c & 1][e];
-                    dv0 = mfma32(s[st], g2.x, dv0);
-                    dv1 = mfma32(s[st], g2.y, dv1);
-                    dk0 = mfma32(dp[st], q2.x, dk0);
-                    dk1 = mfma32(dp[st], q2.y, dk1);
-                }
-                __builtin_amdgcn_sched_barrier(0);
             }
-            wave_lds_sync();
         }
+        __builtin_amdgcn_sched_barrier(0);
+        commit(buf ^ 1);
+        __syncthreads();
+    }
 
-        reduce4(dk0, dk1, dv0, dv1, red, w, lane);
-        if (w == 0)
-        {
-            // register r of lane (n, hf): key k0 + row(r, hf), dims 2n, 2n + 1
+    // register r of lane l: key kw0 + 4 g4 + r, dims 4 c16 + e (accumulator e)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-            {
-                const int key = k0 + mfma_row(r, hf);
-                if (key < T)
-                {
-                    float *dst = gx + (long)key * 3 * C + 2 * n;
-                    *reinterpret_cast<float2 *>(dst + C) = make_float2(dk0[r] * scale, dk1[r] * scale);
-                    *reinterpret_cast<float2 *>(dst + 2 * C) = make_float2(dv0[r], dv1[r]);
-                }
-            }
+    for (int r = 0; r < 4; ++r)
+    {
+        const int key = kw0 + 4 * g4 + r;
+        if (key < T)
+        {
+            float *dst = gx + (long)key * 3 * C + 4 * c16;
+            *reinterpret_cast<float4 *>(dst + C) =
+                make_float4(dk0[r] * scale, dk1[r] * scale, dk2[r] * scale, dk3[r] * scale);
+            *reinterpret_cast<float4 *>(dst + 2 * C) = make_float4(dv0[r], dv1[r], dv2[r], dv3[r]);
         }
     }
 }
@@ -661,6 +605,23 @@ size_t bwd_d64_workspace_bytes(const Shape &s, int *bh_per_chunk)
     return per_bh * (size_t)chunk;
 }
 
+// Compute units of the current device (cached per device; 0 if unknown).
+static int cu_count()
+{
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return 0;
+    if (cached[dev] == 0)
+    {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = -1;
+        cached[dev] = n;
+    }
+    return cached[dev] > 0 ? cached[dev] : 0;
+}
+
 hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
                           const float *qkv, float *ws, int bh_per_chunk, const Shape &s, hipStream_t st)
 {
@@ -678,10 +639,10 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
     for (int bh0 = 0; bh0 < BH; bh0 += bh_per_chunk)
     {
         const int cnt = BH - bh0 < bh_per_chunk ? BH - bh0 : bh_per_chunk;
-        const unsigned blocks = (unsigned)((long)((n_qb + 1) / 2) * cnt);  // heavy/light pairs
         timer_begin(kKindDkdv, st);
-        hipLaunchKernelGGL(bwd_dkdv_d64_kernel, dim3(blocks), dim3(256), 0, st, grad_x, ws, lse, D, dy, qkv, s.T,
-                           s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale);
+        hipLaunchKernelGGL(bwd_dkdv_d64_kernel, dim3((unsigned)((long)((s.T + 63) / 64) * cnt)), dim3(256), 0, st,
+                           grad_x, ws, lse, D, dy, qkv, s.T, s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale,
+                           cu_count());
         timer_end(st);
         const unsigned dq_blocks = (unsigned)((long)((n_qb + 1) / 2 + 3) / 4 * cnt);  // 4 pairs per workgroup
         timer_begin(kKindDq, st);

@@ -30,6 +30,21 @@ __device__ __forceinline__ v16f mfma32(float a, float b, v16f c)
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_f32_16x16x4_f32: D[16x16] += A[16x4] * B[4x16]. Lane l supplies
+// A[l%16][l/16] and B[l/16][l%16]; register r of lane l holds
+// D[4 * (l/16) + r][l%16] (checked on gfx950 with a one-hot probe).
+__device__ __forceinline__ v4f mfma16(float a, float b, v4f c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ v4f zero4()
+{
+    v4f z;
+    z[0] = z[1] = z[2] = z[3] = 0.f;
+    return z;
+}
+
 // Row index of accumulator register r for a lane in half `hf` (= lane / 32).
 __device__ __forceinline__ constexpr int mfma_row(int r, int hf)
 {
