@@ -80,6 +80,27 @@ __device__ __forceinline__ float halves_sum(float x)
     return p.x + p.y;
 }
 
+// v_permlane16_swap with both operands = x: element 0 is x of lane l & ~16,
+// element 1 is x of lane l | 16 (the two 16-lane rows of each 32-lane half),
+// in both lanes of the pair (checked on gfx950).
+__device__ __forceinline__ float2 rows16(float x)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// max / sum of x over lanes l and l ^ 16, the same bits in both lanes.
+__device__ __forceinline__ float rows16_max(float x)
+{
+    const float2 p = rows16(x);
+    return fmaxf(p.x, p.y);
+}
+__device__ __forceinline__ float rows16_sum(float x)
+{
+    const float2 p = rows16(x);
+    return p.x + p.y;
+}
+
 // Compiler-level ordering point between one wave's LDS writes and its reads
 // of other lanes' values (a wave's LDS instructions execute in issue order).
 __device__ __forceinline__ void wave_lds_sync()

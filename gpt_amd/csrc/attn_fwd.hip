@@ -333,6 +333,187 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(3))) vo
         merge_store(1);
 }
 
+// Q-stationary head_dim-64 forward (fwd_qs_d64_kernel). One workgroup per
+// (b, h, 64-query group J); wave w owns the 16 query rows qw0 = 64 J + 16 w ..
+// qw0 + 15: their Q stays in registers as the MFMA B operand and their O, row
+// max and row sum accumulate in registers, so no wave shares a row and nothing
+// is merged. The 4 waves walk the key blocks 0 .. 2J + 1 together; each
+// block's K and V (32 x 64) are staged once in LDS for all 4 waves (double
+// buffered: block kb + 1 is loaded into registers while block kb is computed,
+// then written to the other buffer; one barrier per block). Per wave and key
+// block, on v_mfma_f32_16x16x4_f32 (two 16-key tiles kt):
+//   S^T_kt = K_kt Q^T          (16 keys x 16 queries, 16 MFMAs each)
+//   online softmax per query column (8 values per lane, then across the 4
+//   lane groups), in log2 units with the scale folded into the exponent FMA
+//   O^T += V^T P^T             (4 accumulators of 16 x 16 over 32 keys; the
+//                              S^T accumulators are the B operands as they are)
+// Workgroups are ordered heaviest first (J descending), (b, h) fastest; when
+// the whole grid is resident the middle round is reversed (in blocks of 8, one
+// XCD per (b, h)) so that every CU gets one heavy, one light and one middle
+// group.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void fwd_qs_d64_kernel(
+    float *__restrict__ y, float *__restrict__ lse, const float *__restrict__ qkv, int T, int C, int H, int BH,
+    int n_qg, float c2, int n_cu)
+{
+    constexpr int ST = kRowStride;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+    const int c16 = lane & 15, g4 = lane >> 4;
+    int item = (int)blockIdx.x;
+    {
+        const int G = (int)gridDim.x;
+        if (n_cu > 0 && n_cu % 8 == 0 && G % n_cu == 0 && G / n_cu <= 3)
+        {
+            const int r = item / n_cu;
+            int c = item % n_cu;
+            if (r & 1)
+                c = (n_cu / 8 - 1 - c / 8) * 8 + (c & 7);
+            item = r * n_cu + c;
+        }
+    }
+    const int J = n_qg - 1 - item / BH;
+    const int bh = item % BH;
+    const int b = bh / H, h = bh % H;
+    const int qw0 = 64 * J + 16 * w;
+    const uint32_t Wb = 12u * (uint32_t)C, Cb = 4u * (uint32_t)C;
+    const rsrc_t rs = make_rsrc(qkv + (long)b * T * 3L * C + (long)h * 64,
+                                (uint32_t)(((long)T * 3 * C - (long)h * 64) * 4));
+
+    __shared__ __attribute__((aligned(16))) float sk[2][32 * ST], sv[2][32 * ST];
+
+    // stationary B operand: lane l holds Q[qw0 + l%16][16 (l/16) + m], m = 0..15
+    // (MFMA m contracts d = m + 16 kk, kk = l/16)
+    float qreg[16];
+    {
+        const uint32_t off = (uint32_t)c16 * Wb + 64u * g4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+        {
+            const float4 q4 = bload4s(rs, off + 16u * c, (uint32_t)qw0 * Wb);
+            qreg[4 * c + 0] = q4.x;
+            qreg[4 * c + 1] = q4.y;
+            qreg[4 * c + 2] = q4.z;
+            qreg[4 * c + 3] = q4.w;
+        }
+    }
+
+    // staging: thread tid moves float4s tid and tid + 256 of the K and V tiles
+    // (row = idx / 16, column 4 (idx % 16))
+    const int r0 = tid >> 4, cc = tid & 15;
+    const uint32_t st_k = (uint32_t)r0 * Wb + Cb + 16u * cc;
+    float4 pk[2], pv[2];
+    const int kb_end = min(2 * J + 2, (T + 31) / 32);  // key blocks 0 .. kb_end - 1
+    auto issue = [&](int kb) {
+        const uint32_t ko = kb < kb_end ? 32u * (uint32_t)kb * Wb : kNoBlock;
+        pk[0] = bload4s(rs, st_k, ko);
+        pk[1] = bload4s(rs, st_k + 16u * Wb, ko);
+        pv[0] = bload4s(rs, st_k + Cb, ko);
+        pv[1] = bload4s(rs, st_k + Cb + 16u * Wb, ko);
+    };
+    auto commit = [&](int buf) {
+        *reinterpret_cast<float4 *>(&sk[buf][r0 * ST + 4 * cc]) = pk[0];
+        *reinterpret_cast<float4 *>(&sk[buf][(r0 + 16) * ST + 4 * cc]) = pk[1];
+        *reinterpret_cast<float4 *>(&sv[buf][r0 * ST + 4 * cc]) = pv[0];
+        *reinterpret_cast<float4 *>(&sv[buf][(r0 + 16) * ST + 4 * cc]) = pv[1];
+    };
+
+    v4f o0 = zero4(), o1 = zero4(), o2 = zero4(), o3 = zero4();  // O^T, d = 16 g4 + 4 r + e
+    float m = -INFINITY, l = 0.f;  // running max (log2 units) and sum of query qw0 + c16
+    issue(0);
+    commit(0);
+    __syncthreads();
+    for (int kb = 0; kb < kb_end; ++kb)
+    {
+        const int buf = kb & 1;
+        issue(kb + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        const int k0 = 32 * kb;
+        if (k0 <= qw0 + 15)  // else every key of the block lies past this wave's queries
+        {
+            const float *Ks = sk[buf], *Vs = sv[buf];
+            // S^T_kt[key k0 + 16 kt + 4 g4 + r][query qw0 + c16] (unscaled)
+            v4f s0 = zero4(), s1 = zero4();
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+            {
+                const float4 ka = *reinterpret_cast<const float4 *>(Ks + c16 * ST + 16 * g4 + 4 * c);
+                const float4 kb4 = *reinterpret_cast<const float4 *>(Ks + (16 + c16) * ST + 16 * g4 + 4 * c);
+                const float kav[4] = {ka.x, ka.y, ka.z, ka.w}, kbv[4] = {kb4.x, kb4.y, kb4.z, kb4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                {
+                    s0 = mfma16(kav[e], qreg[4 * c + e], s0);
+                    s1 = mfma16(kbv[e], qreg[4 * c + e], s1);
+                }
+            }
+            if (k0 + 31 > qw0)
+            {
+                // diagonal block: key > query is masked out
+                const int q = qw0 + c16;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                {
+                    if (k0 + 4 * g4 + r > q)
+                        s0[r] = -INFINITY;
+                    if (k0 + 16 + 4 * g4 + r > q)
+                        s1[r] = -INFINITY;
+                }
+            }
+            float mt = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                             fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+            mt = halves_max(rows16_max(mt));
+            const float mn = fmaxf(m, mt * c2);
+            const float corr = fast_exp2(m - mn);
+            float ps = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+            {
+                s0[r] = fast_exp2(fmaf(s0[r], c2, -mn));
+                s1[r] = fast_exp2(fmaf(s1[r], c2, -mn));
+                ps += s0[r] + s1[r];
+            }
+            l = l * corr + halves_sum(rows16_sum(ps));
+            m = mn;
+            o0 *= corr;
+            o1 *= corr;
+            o2 *= corr;
+            o3 *= corr;
+            // O^T += V^T P^T: step (kt, r) contracts keys k0 + 16 kt + 4 kk + r
+            // (kk = l/16); A operand V[that key][4 c16 + e]
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+            {
+                const float4 va = *reinterpret_cast<const float4 *>(Vs + (4 * g4 + r) * ST + 4 * c16);
+                const float4 vb = *reinterpret_cast<const float4 *>(Vs + (16 + 4 * g4 + r) * ST + 4 * c16);
+                o0 = mfma16(va.x, s0[r], o0);
+                o1 = mfma16(va.y, s0[r], o1);
+                o2 = mfma16(va.z, s0[r], o2);
+                o3 = mfma16(va.w, s0[r], o3);
+                o0 = mfma16(vb.x, s1[r], o0);
+                o1 = mfma16(vb.y, s1[r], o1);
+                o2 = mfma16(vb.z, s1[r], o2);
+                o3 = mfma16(vb.w, s1[r], o3);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        commit(buf ^ 1);
+        __syncthreads();
+    }
+
+    // register r of accumulator e: O[qw0 + c16][16 g4 + 4 r + e]
+    const int row = qw0 + c16;
+    if (row < T)
+    {
+        const float inv = 1.f / l;
+        float *dst = y + ((long)b * T + row) * C + (long)h * 64 + 16 * g4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            *reinterpret_cast<float4 *>(dst + 4 * r) =
+                make_float4(o0[r] * inv, o1[r] * inv, o2[r] * inv, o3[r] * inv);
+        if (g4 == 0)
+            lse[((long)b * T + row) * H + h] = (m + fast_log2(l)) * kLn2;
+    }
+}
+
 // General head_dim (1..DM): one thread per (b, h, query row), online softmax
 // over keys 0..i, q and the output row in registers.
 template <int DM>
@@ -389,6 +570,22 @@ __global__ __launch_bounds__(128) void fwd_general_kernel(float *__restrict__ y,
 
 static float softmax_scale(int d) { return 1.0f / sqrtf((float)d); }
 
+static int fwd_cu_count()
+{
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return 0;
+    if (cached[dev] == 0)
+    {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = -1;
+        cached[dev] = n;
+    }
+    return cached[dev] > 0 ? cached[dev] : 0;
+}
+
 hipError_t launch_fwd_d64(float *y, float *lse, const float *qkv, const Shape &s, hipStream_t st)
 {
     const int n_qb = (s.T + 31) / 32;
@@ -405,6 +602,15 @@ hipError_t launch_fwd_d64(float *y, float *lse, const float *qkv, const Shape &s
     if (n_qb == 1)
         nw = 1;
     timer_begin(kKindFwd, st);
+    const int n_qg = (s.T + 63) / 64;
+    if ((long)n_qg * BH >= 256)
+    {
+        // enough 64-query groups to fill the GPU: the Q-stationary kernel
+        hipLaunchKernelGGL(fwd_qs_d64_kernel, dim3((unsigned)((long)n_qg * BH)), dim3(256), 0, st, y, lse, qkv, s.T,
+                           s.C, s.H, BH, n_qg, c2, fwd_cu_count());
+        timer_end(st);
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)blocks);
     switch (nw)
     {
