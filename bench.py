@@ -64,7 +64,7 @@ def attn_flops(b, t, h, d, fwd=True, bwd=True):
 # dK/dV kernel S + dP + dV + dK = 4; dQ kernel dS K = 1. The D-row kernel does
 # no matrix work (bandwidth-bound: reads dO and O).
 KERNEL_FLOP_UNITS = {"fwd": 2, "bwd_dkdv": 4, "bwd_dq": 1, "bwd_rowdot": 0}
-KERNEL_SYMBOL = {"fwd": "fwd_d64_kernel", "bwd_dkdv": "bwd_dkdv_d64_kernel", "bwd_dq": "bwd_dq_d64_kernel",
+KERNEL_SYMBOL = {"fwd": "fwd_qs_d64_kernel", "bwd_dkdv": "bwd_dkdv_d64_kernel", "bwd_dq": "bwd_dq_d64_kernel",
                  "bwd_rowdot": "bwd_rowdot_d64_kernel"}
 COPY_BYTES = 256 << 20
 

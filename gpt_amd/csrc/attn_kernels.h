@@ -15,7 +15,7 @@ struct Shape
 // Kernel kinds reported by the optional launch timer (gpt_hip_attn_timing_*).
 enum KernelKind
 {
-    kKindFwd = 0,       // fwd_d64_kernel
+    kKindFwd = 0,       // fwd_qs_d64_kernel / fwd_d64_kernel
     kKindRowdot = 1,    // bwd_rowdot_d64_kernel
     kKindDkdv = 2,      // bwd_dkdv_d64_kernel
     kKindDq = 3,        // bwd_dq_d64_kernel
