@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     const float *__restrict__ Dv, const float *__restrict__ dy, const float *__restrict__ qkv, int T, int C, int H,
     int bh0, int BHc, int n_qb, float c2, float scale, int n_cu)
 {
-    constexpr int ST = kRowStride;
+    constexpr int ST = kTileRow;
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int c16 = lane & 15, g4 = lane >> 4;
     // Work item = (key group J, (b, h)), heaviest first: J-major, (b, h)
@@ -176,7 +176,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     float *ws = dsw + (long)bhl * ((long)n_qb * (n_qb + 1) / 2) * 1024;
     float *gx = grad_x + (long)b * T * 3L * C + (long)h * 64;
 
-    __shared__ __attribute__((aligned(16))) float sq[2][32 * ST], so[2][32 * ST];  // Q, dO of the block
+    // Q, dO of the block, swizzled (tile_off)
+    __shared__ __attribute__((aligned(16))) float sq[2][32 * ST], so[2][32 * ST];
     __shared__ __attribute__((aligned(16))) float sl[2][32], sd[2][32];             // lse * log2(e), D
 
     // stationary B operands: lane l holds K / V[kw0 + l%16][16 (l/16) + m],
@@ -204,7 +205,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     // tiles (row = idx / 16, column 4 (idx % 16)); threads 0..31 an lse row,
     // 32..63 a D row
     constexpr int NT = 256, NU = 512 / NT;
-    const int r0 = tid >> 4, cc = tid & 15;
+    const int r0 = tid >> 4, cc = tid & 15, t_st = tile_off(r0, cc);
     const uint32_t st_q = (uint32_t)r0 * Wb + 16u * cc, st_o = (uint32_t)r0 * Cb + 16u * cc;
     float4 pq[NU], po[NU];
     float pld = 0.f;
@@ -227,8 +228,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
 #pragma unroll
         for (int u = 0; u < NU; ++u)
         {
-            *reinterpret_cast<float4 *>(&sq[buf][(r0 + u * NT / 16) * ST + 4 * cc]) = pq[u];
-            *reinterpret_cast<float4 *>(&so[buf][(r0 + u * NT / 16) * ST + 4 * cc]) = po[u];
+            *reinterpret_cast<float4 *>(&sq[buf][(u * NT / 16) * ST + t_st]) = pq[u];
+            *reinterpret_cast<float4 *>(&so[buf][(u * NT / 16) * ST + t_st]) = po[u];
         }
         if (tid < 32)
             sl[buf][tid] = pld;
@@ -256,10 +257,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
 #pragma unroll
             for (int c = 0; c < 4; ++c)
             {
-                const float4 qa0 = *reinterpret_cast<const float4 *>(Qs + c16 * ST + 16 * g4 + 4 * c);
-                const float4 qa1 = *reinterpret_cast<const float4 *>(Qs + (16 + c16) * ST + 16 * g4 + 4 * c);
-                const float4 oa0 = *reinterpret_cast<const float4 *>(Os + c16 * ST + 16 * g4 + 4 * c);
-                const float4 oa1 = *reinterpret_cast<const float4 *>(Os + (16 + c16) * ST + 16 * g4 + 4 * c);
+                const int ta = tile_off(c16, 4 * g4 + c);
+                const float4 qa0 = *reinterpret_cast<const float4 *>(Qs + ta);
+                const float4 qa1 = *reinterpret_cast<const float4 *>(Qs + 16 * ST + ta);
+                const float4 oa0 = *reinterpret_cast<const float4 *>(Os + ta);
+                const float4 oa1 = *reinterpret_cast<const float4 *>(Os + 16 * ST + ta);
                 const float q0v[4] = {qa0.x, qa0.y, qa0.z, qa0.w}, q1v[4] = {qa1.x, qa1.y, qa1.z, qa1.w};
                 const float o0v[4] = {oa0.x, oa0.y, oa0.z, oa0.w}, o1v[4] = {oa1.x, oa1.y, oa1.z, oa1.w};
 #pragma unroll
@@ -311,9 +313,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                 {
-                    const int row = 16 * t + 4 * g4 + r;
-                    const float4 ob = *reinterpret_cast<const float4 *>(Os + row * ST + 4 * c16);
-                    const float4 qb = *reinterpret_cast<const float4 *>(Qs + row * ST + 4 * c16);
+                    const int tb = tile_off(16 * t + 4 * g4 + r, c16);
+                    const float4 ob = *reinterpret_cast<const float4 *>(Os + tb);
+                    const float4 qb = *reinterpret_cast<const float4 *>(Qs + tb);
                     const float ap = t == 0 ? s0[r] : s1[r], ad = t == 0 ? p0[r] : p1[r];
                     dv0 = mfma16(ap, ob.x, dv0);
                     dv1 = mfma16(ap, ob.y, dv1);

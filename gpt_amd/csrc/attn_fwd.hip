@@ -355,7 +355,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
     float *__restrict__ y, float *__restrict__ lse, const float *__restrict__ qkv, int T, int C, int H, int BH,
     int n_qg, float c2, int n_cu)
 {
-    constexpr int ST = kRowStride;
+    constexpr int ST = kTileRow;
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int c16 = lane & 15, g4 = lane >> 4;
     int item = (int)blockIdx.x;
@@ -378,6 +378,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
     const rsrc_t rs = make_rsrc(qkv + (long)b * T * 3L * C + (long)h * 64,
                                 (uint32_t)(((long)T * 3 * C - (long)h * 64) * 4));
 
+    // K tiles swizzled (tile_off), V tiles plain 64-word rows: the V reads
+    // (row 4 (l/16) + r, column group l%16) are conflict-free unswizzled
     __shared__ __attribute__((aligned(16))) float sk[2][32 * ST], sv[2][32 * ST];
 
     // stationary B operand: lane l holds Q[qw0 + l%16][16 (l/16) + m], m = 0..15
@@ -398,7 +400,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
 
     // staging: thread tid moves float4s tid and tid + 256 of the K and V tiles
     // (row = idx / 16, column 4 (idx % 16))
-    const int r0 = tid >> 4, cc = tid & 15;
+    const int r0 = tid >> 4, cc = tid & 15, k_st = tile_off(r0, cc);
     const uint32_t st_k = (uint32_t)r0 * Wb + Cb + 16u * cc;
     float4 pk[2], pv[2];
     const int kb_end = min(2 * J + 2, (T + 31) / 32);  // key blocks 0 .. kb_end - 1
@@ -410,8 +412,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
         pv[1] = bload4s(rs, st_k + Cb + 16u * Wb, ko);
     };
     auto commit = [&](int buf) {
-        *reinterpret_cast<float4 *>(&sk[buf][r0 * ST + 4 * cc]) = pk[0];
-        *reinterpret_cast<float4 *>(&sk[buf][(r0 + 16) * ST + 4 * cc]) = pk[1];
+        *reinterpret_cast<float4 *>(&sk[buf][k_st]) = pk[0];
+        *reinterpret_cast<float4 *>(&sk[buf][16 * ST + k_st]) = pk[1];
         *reinterpret_cast<float4 *>(&sv[buf][r0 * ST + 4 * cc]) = pv[0];
         *reinterpret_cast<float4 *>(&sv[buf][(r0 + 16) * ST + 4 * cc]) = pv[1];
     };
@@ -435,8 +437,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
 #pragma unroll
             for (int c = 0; c < 4; ++c)
             {
-                const float4 ka = *reinterpret_cast<const float4 *>(Ks + c16 * ST + 16 * g4 + 4 * c);
-                const float4 kb4 = *reinterpret_cast<const float4 *>(Ks + (16 + c16) * ST + 16 * g4 + 4 * c);
+                const int ko = tile_off(c16, 4 * g4 + c);
+                const float4 ka = *reinterpret_cast<const float4 *>(Ks + ko);
+                const float4 kb4 = *reinterpret_cast<const float4 *>(Ks + 16 * ST + ko);
                 const float kav[4] = {ka.x, ka.y, ka.z, ka.w}, kbv[4] = {kb4.x, kb4.y, kb4.z, kb4.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
