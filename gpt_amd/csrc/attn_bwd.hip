@@ -224,7 +224,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
         else if (tid < 64)
             pld = bload1s(rd, (uint32_t)(tid - 32) * Hb, lo);
     };
-    auto commit = [&](int buf) {
+    auto commit = [&](auto buf_c) {
+        constexpr int buf = decltype(buf_c)::value;
 #pragma unroll
         for (int u = 0; u < NU; ++u)
         {
@@ -241,11 +242,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     v4f dv0 = zero4(), dv1 = zero4(), dv2 = zero4(), dv3 = zero4();
     const int i_lo = 2 * J;
     issue(i_lo);
-    commit(0);
+    commit(BufIdx<0>{});
     __syncthreads();
-    for (int i = i_lo; i < n_qb; ++i)
-    {
-        const int buf = (i - i_lo) & 1;
+    // one query block; the LDS buffer index is a compile-time constant (the
+    // loop below is unrolled by two) so that it folds into the ds_read offsets
+    auto step = [&](const int i, auto buf_c) {
+        constexpr int buf = decltype(buf_c)::value;
         issue(i + 1);
         __builtin_amdgcn_sched_barrier(0);
         const int q0 = 32 * i;
@@ -273,8 +275,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                     p1 = mfma16(o1v[e], vreg[4 * c + e], p1);
                 }
             }
-            // P and dS (without the 1/sqrt(d)); zero where key > query or the
-            // query row is past T
+            // P and dS (without the 1/sqrt(d)); zero where key > query. Rows
+            // past T need no mask: their Q, dO, lse and D load as zeros, so
+            // P = 1 and dS = 0 there and they add nothing to dK, dV or dQ.
             {
                 const float4 L0 = *reinterpret_cast<const float4 *>(&sl[buf][4 * g4]);
                 const float4 L1 = *reinterpret_cast<const float4 *>(&sl[buf][16 + 4 * g4]);
@@ -282,17 +285,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                 const float4 D1 = *reinterpret_cast<const float4 *>(&sd[buf][16 + 4 * g4]);
                 const float l0v[4] = {L0.x, L0.y, L0.z, L0.w}, l1v[4] = {L1.x, L1.y, L1.z, L1.w};
                 const float d0v[4] = {D0.x, D0.y, D0.z, D0.w}, d1v[4] = {D1.x, D1.y, D1.z, D1.w};
-                const int key = kw0 + c16;
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                 {
-                    const int qa = q0 + 4 * g4 + r, qb = qa + 16;
-                    const bool ka = key <= qa && qa < T, kb = key <= qb && qb < T;
-                    const float pa = fast_exp2(s0[r] * c2 - l0v[r]), pb = fast_exp2(s1[r] * c2 - l1v[r]);
-                    s0[r] = ka ? pa : 0.f;
-                    p0[r] = ka ? pa * (p0[r] - d0v[r]) : 0.f;
-                    s1[r] = kb ? pb : 0.f;
-                    p1[r] = kb ? pb * (p1[r] - d1v[r]) : 0.f;
+                    const float pa = fast_exp2(fmaf(s0[r], c2, -l0v[r])), pb = fast_exp2(fmaf(s1[r], c2, -l1v[r]));
+                    s0[r] = pa;
+                    p0[r] = pa * (p0[r] - d0v[r]);
+                    s1[r] = pb;
+                    p1[r] = pb * (p1[r] - d1v[r]);
+                }
+                if (q0 < kw0 + 15)  // some key of this wave lies past some query of the block
+                {
+                    const int key = kw0 + c16;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                    {
+                        const int qa = q0 + 4 * g4 + r, qb = qa + 16;
+                        if (key > qa)
+                            s0[r] = p0[r] = 0.f;
+                        if (key > qb)
+                            s1[r] = p1[r] = 0.f;
+                    }
                 }
             }
             // this wave's 32 x 16 half of dS tile (i, kw0 / 32), query-major
@@ -329,9 +342,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        commit(buf ^ 1);
+        commit(BufIdx<buf ^ 1>{});
         __syncthreads();
+    };
+    int i = i_lo;
+    for (; i + 1 < n_qb; i += 2)
+    {
+        step(i, BufIdx<0>{});
+        step(i + 1, BufIdx<1>{});
     }
+    if (i < n_qb)
+        step(i, BufIdx<0>{});
 
     // register r of lane l: key kw0 + 4 g4 + r, dims 4 c16 + e (accumulator e)
 #pragma unroll

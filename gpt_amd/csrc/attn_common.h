@@ -15,6 +15,10 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+// Lazy online-softmax rescaling: probabilities are taken against a reference
+// max that may lag the running max by up to this much (log2 units), so they
+// stay <= 2^8 and fp32 sums of them cannot overflow for any T < 2^100.
+constexpr float kLazyRescale = 8.f;
 
 // LDS row stride (floats) for the 64-wide fp32 tiles of the 32x32x2 kernels:
 // their row reads (one row per lane of a half-wave) measured free of bank
@@ -177,6 +181,13 @@ __device__ __forceinline__ float bload1s(rsrc_t r, uint32_t voff, uint32_t soff)
 
 // Index of the calling wave in its workgroup, as a value the compiler knows
 // to be wave-uniform (so offsets derived from it can live in SGPRs).
+// Compile-time index (of an LDS double buffer) passed to generic lambdas.
+template <int N>
+struct BufIdx
+{
+    static constexpr int value = N;
+};
+
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 __device__ __forceinline__ v16f zero16()

@@ -343,10 +343,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(3))) vo
 // then written to the other buffer; one barrier per block). Per wave and key
 // block, on v_mfma_f32_16x16x4_f32 (two 16-key tiles kt):
 //   S^T_kt = K_kt Q^T          (16 keys x 16 queries, 16 MFMAs each)
-//   online softmax per query column (8 values per lane, then across the 4
-//   lane groups), in log2 units with the scale folded into the exponent FMA
+//   online softmax per query column in log2 units, the scale folded into the
+//   exponent FMA, with a lazily updated reference max m: while no score of
+//   the block exceeds m + kLazyRescale (checked with one wave vote), P is taken
+//   against the stale m (so P <= 2^kLazyRescale) and neither O nor the row
+//   sums are rescaled; otherwise m is raised to the block's row max (reduced
+//   across the 4 lane groups) and O and the sums are rescaled. The quotient
+//   O / l and lse = m + log2 l do not depend on which m was used.
 //   O^T += V^T P^T             (4 accumulators of 16 x 16 over 32 keys; the
 //                              S^T accumulators are the B operands as they are)
+// Each lane keeps the row sum over its own keys; the 4 lane groups' sums are
+// added once, after the last block.
 // Workgroups are ordered heaviest first (J descending), (b, h) fastest; when
 // the whole grid is resident the middle round is reversed (in blocks of 8, one
 // XCD per (b, h)) so that every CU gets one heavy, one light and one middle
@@ -419,7 +426,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
     };
 
     v4f o0 = zero4(), o1 = zero4(), o2 = zero4(), o3 = zero4();  // O^T, d = 16 g4 + 4 r + e
-    float m = -INFINITY, l = 0.f;  // running max (log2 units) and sum of query qw0 + c16
+    // reference max (log2 units, the same in the 4 lane groups of a query) of
+    // query qw0 + c16 and this lane's part of its row sum
+    float m = -INFINITY, l = 0.f;
     issue(0);
     commit(0);
     __syncthreads();
@@ -461,25 +470,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
                         s1[r] = -INFINITY;
                 }
             }
-            float mt = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
-                             fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
-            mt = halves_max(rows16_max(mt));
-            const float mn = fmaxf(m, mt * c2);
-            const float corr = fast_exp2(m - mn);
-            float ps = 0.f;
+            // exponent arguments against the current reference max
+            float e0[4], e1[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
             {
-                s0[r] = fast_exp2(fmaf(s0[r], c2, -mn));
-                s1[r] = fast_exp2(fmaf(s1[r], c2, -mn));
-                ps += s0[r] + s1[r];
+                e0[r] = fmaf(s0[r], c2, -m);
+                e1[r] = fmaf(s1[r], c2, -m);
             }
-            l = l * corr + halves_sum(rows16_sum(ps));
-            m = mn;
-            o0 *= corr;
-            o1 *= corr;
-            o2 *= corr;
-            o3 *= corr;
+            const float emax = fmaxf(fmaxf(fmaxf(e0[0], e0[1]), fmaxf(e0[2], e0[3])),
+                                     fmaxf(fmaxf(e1[0], e1[1]), fmaxf(e1[2], e1[3])));
+            // The first block always takes this branch: with m = -inf every
+            // lane holding an unmasked score has emax = +inf, and key 0 is
+            // unmasked for every query (lanes with only masked scores get
+            // NaN arguments here, which the branch recomputes). m is finite
+            // afterwards.
+            if (__any(emax > kLazyRescale))
+            {
+                const float mt = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                                       fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]))) * c2;
+                const float mn = fmaxf(m, halves_max(rows16_max(mt)));
+                const float corr = fast_exp2(m - mn);
+                l *= corr;
+                m = mn;
+                o0 *= corr;
+                o1 *= corr;
+                o2 *= corr;
+                o3 *= corr;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                {
+                    e0[r] = fmaf(s0[r], c2, -m);
+                    e1[r] = fmaf(s1[r], c2, -m);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+            {
+                s0[r] = fast_exp2(e0[r]);
+                s1[r] = fast_exp2(e1[r]);
+            }
+            l += ((s0[0] + s1[0]) + (s0[1] + s1[1])) + ((s0[2] + s1[2]) + (s0[3] + s1[3]));
             // O^T += V^T P^T: step (kt, r) contracts keys k0 + 16 kt + 4 kk + r
             // (kk = l/16); A operand V[that key][4 c16 + e]
 #pragma unroll
@@ -503,6 +534,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
     }
 
     // register r of accumulator e: O[qw0 + c16][16 g4 + 4 r + e]
+    l = halves_sum(rows16_sum(l));
     const int row = qw0 + c16;
     if (row < T)
     {
