@@ -93,6 +93,29 @@ def test_ragged_T_fwd_bwd(dev, T):
     check_fwd_bwd(dev, x, g, H, tag=f"T={T}")
 
 
+@pytest.mark.parametrize("T", [256, 300])
+def test_growing_scores_fwd_bwd(dev, T):
+    """Scores that step up by 50 (about 9 in log2 units, past the forward's
+    lazy-rescale margin of 8) at several keys, block-aligned in head 0 and
+    not in head 1, so the running max rises after the first key block and
+    the kernels must rescale O mid-row; head 2 keeps random scores."""
+    B, C, H, d = 2, 192, 3, 64
+    x = synth.qkv(B, T, C, seed=4242 + T)
+    g = synth.grad_out(B, T, C, seed=4242 + T, std=1.0)
+    rng = np.random.default_rng(17)
+    for h, steps in ((0, (64, 128, 192, 256)), (1, (40, 100, 170, 230, 290))):
+        u = rng.standard_normal(d).astype(np.float32)
+        u /= np.linalg.norm(u)
+        level = np.zeros(T, np.float32)
+        for s in steps:
+            level[s:] += 6.25  # q . k steps by 8 * 6.25 = 50
+        for b in range(B):
+            x[b, :, h * d:(h + 1) * d] = 8.0 * u
+            x[b, :, C + h * d:C + (h + 1) * d] = (level[:, None] * u[None, :]
+                                                  + 0.1 * rng.standard_normal((T, d)).astype(np.float32))
+    check_fwd_bwd(dev, x, g, H, tag=f"growing T={T}")
+
+
 def test_config5b_prefix_sweep_T1_to_256(dev):
     """Forward at B=1 for every prefix length 1..256, as autoregressive
     generation without a KV cache does."""
