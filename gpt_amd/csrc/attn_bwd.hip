@@ -369,30 +369,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     }
 }
 
-// dQ_i = scale * sum_{j<=i} dS_ij K_j. One WAVE per (b, h, query-block pair
-// (n - 1 - p, p)): n + 1 units, run as one stream (the heavy block's key
-// blocks 0..n-1-p, then the light block's 0..p), so no wave ever waits for
-// another and nothing is merged. A unit's operands (the dS tile and the K
-// block, 12 KiB) are loaded one unit ahead into a second register set while
-// the current unit's 32 MFMAs run. Workgroups hold 4 waves = 4 pairs of one
-// (b, h), ordered (chunk of pairs)-major with (b, h) fastest, the same
-// (b, h) -> XCD mapping as the dK/dV kernel, so a (b, h)'s dS tiles are read
-// from the L2 they were written to.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void bwd_dq_d64_kernel(float *__restrict__ grad_x,
+// dQ_i = scale * sum_{j<=i} dS_ij K_j. One workgroup per (b, h, query-block
+// pair (n - 1 - p, p)). Each block's units (its key blocks 0..i) are split
+// into 4 contiguous ranges, one per wave (spare units of the heavy block go to
+// the first waves, of the light block to the last, so that no wave gets two),
+// and every dS tile and K block is loaded once. A wave walks its heavy range,
+// then its light range, as one stream on v_mfma_f32_32x32x2_f32 (16 MFMAs
+// per half-unit of 16 keys, whose operands are loaded one half-unit ahead),
+// keeping its partial dQ (32 x 64) of the current block in registers; the 4
+// waves' partials are added through LDS at the end, in a fixed order, and
+// the blocks' rows are stored. Workgroups are ordered pair-major with
+// (b, h) fastest, the same (b, h) -> XCD mapping as the dK/dV kernel, so a
+// (b, h)'s dS tiles are read from the L2 they were written to.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void bwd_dq_d64_kernel(float *__restrict__ grad_x,
                                                          const float *__restrict__ dsw,
                                                          const float *__restrict__ qkv,
                                                          int T, int C, int H, int bh0, int BHc, int n_qb,
                                                          float scale)
 {
-    const int lane = threadIdx.x & 63, w = wave_id();
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int n = lane & 31, hf = lane >> 5;
-    const int chunk = (int)(blockIdx.x / BHc);
+    const int pr = (int)(blockIdx.x / BHc);  // this workgroup's pair
     const int bhl = (int)(blockIdx.x % BHc), bh = bh0 + bhl;
     const int b = bh / H, h = bh % H;
-    const int pr = 4 * chunk + w;  // this wave's pair
-    const int n_pairs = (n_qb + 1) / 2;
-    if (pr >= n_pairs)
-        return;
     const int qa = n_qb - 1 - pr;
     const bool two = qa != pr;
     const uint32_t Wb = 12u * (uint32_t)C;
@@ -405,36 +404,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
     const uint32_t w_lane = (uint32_t)n * 128u + 64u * hf;
     const uint32_t k_lane = 16u * hf * Wb + 8u * (uint32_t)n;
 
-    // unit u of the stream: query block i(u), key block j(u)
-    const int cnt0 = qa + 1, total = cnt0 + (two ? pr + 1 : 0);
-    auto tile_off = [&](int u) -> uint32_t {
-        if (u >= total)
-            return kNoBlock;
-        const int i = u < cnt0 ? qa : pr, j = u < cnt0 ? u : u - cnt0;
-        return (uint32_t)(((long)i * (i + 1) / 2 + j) * 4096);
+    // this wave's key blocks: [ja0, ja1) of block qa, then [jb0, jb1) of block pr
+    auto range = [](int cnt, int slot, int &j0, int &j1) {
+        const int q = cnt / 4, r = cnt % 4;
+        j0 = slot * q + (slot < r ? slot : r);
+        j1 = j0 + q + (slot < r ? 1 : 0);
     };
-    auto key_off = [&](int u) -> uint32_t {
-        if (u >= total)
-            return kNoBlock;
-        return 32u * (uint32_t)(u < cnt0 ? u : u - cnt0) * Wb;
+    int ja0, ja1, jb0 = 0, jb1 = 0;
+    range(qa + 1, w, ja0, ja1);
+    if (two)
+        range(pr + 1, 3 - w, jb0, jb1);
+    const int na = ja1 - ja0, nu = na + (jb1 - jb0);
+    // unit v of the wave's stream (branch-free, wave-uniform, in SGPRs)
+    const uint32_t base_a = ((uint32_t)qa * (uint32_t)(qa + 1) / 2u + (uint32_t)ja0) * 4096u;
+    const uint32_t base_b = ((uint32_t)pr * (uint32_t)(pr + 1) / 2u + (uint32_t)jb0 - (uint32_t)na) * 4096u;
+    auto tile_at = [&](int v) -> uint32_t {
+        const uint32_t o = (v < na ? base_a : base_b) + (uint32_t)v * 4096u;
+        return v < nu ? o : kNoBlock;
+    };
+    auto key_at = [&](int v) -> uint32_t {
+        const int j = v < na ? ja0 + v : jb0 + v - na;
+        return v < nu ? 32u * (uint32_t)j * Wb : kNoBlock;
     };
 
-    // Two operand sets, A and B: unit u uses set u % 2; the next unit's set
-    // is loaded while this unit's MFMAs run. (Deeper prefetch does not pay at
-    // B=16, T=256: the kernel is bound by the dS / K reads, not by latency.)
-    float4 dsA[4], dsB[4];   // A operand dS[n][16 hf + t], t = 0..15
-    float2 kkA[16], kkB[16]; // B operand K[32j + 16 hf + t][2n, 2n + 1]
-#define DQ_LOAD(DS, KK, u)                                                        \
+    // Half-units: half x (x = 0, 1) of a unit contracts keys 16 hf + 8 x + t
+    // (t = 0..7) for k-slot hf, in 16 MFMAs; its operands are
+    //   ds[e] = dS[n][16 hf + 8 x + 4 e ..]  (e = 0, 1; MFMA A operand)
+    //   kk[t] = K[32 j + 16 hf + 8 x + t][2n, 2n + 1]  (B operand)
+    // and are prefetched one half-unit ahead (two sets, 24 VGPRs each).
+    float4 dsA[2], dsB[2];
+    float2 kkA[8], kkB[8];
+#define DQ_LOAD(DS, KK, v)                                                        \
     do                                                                            \
     {                                                                             \
-        const uint32_t to_ = tile_off(u), ko_ = key_off(u);                       \
-        _Pragma("unroll") for (int e = 0; e < 4; ++e) DS[e] = bload4s(rw, w_lane + 16u * e, to_); \
-        _Pragma("unroll") for (int t = 0; t < 16; ++t) KK[t] = bload2s(rk, k_lane, ko_ + (uint32_t)t * Wb); \
+        const int x_ = (v) & 1;                                                   \
+        const uint32_t to_ = tile_at((v) >> 1), ko_ = key_at((v) >> 1) + 8u * (uint32_t)x_ * Wb; \
+        _Pragma("unroll") for (int e = 0; e < 2; ++e) DS[e] = bload4s(rw, w_lane + 32u * x_ + 16u * e, to_); \
+        _Pragma("unroll") for (int t = 0; t < 8; ++t) KK[t] = bload2s(rk, k_lane, ko_ + (uint32_t)t * Wb); \
     } while (0)
 #define DQ_MFMA(DS, KK)                                                           \
     do                                                                            \
     {                                                                             \
-        _Pragma("unroll") for (int e = 0; e < 4; ++e)                             \
+        _Pragma("unroll") for (int e = 0; e < 2; ++e)                             \
         {                                                                         \
             a0 = mfma32(DS[e].x, KK[4 * e + 0].x, a0);                            \
             a1 = mfma32(DS[e].x, KK[4 * e + 0].y, a1);                            \
@@ -447,40 +458,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
         }                                                                         \
     } while (0)
     v16f a0 = zero16(), a1 = zero16();
-    // last unit of a query block: register r of lane (n, hf) holds
-    // dQ[32 i + row(r, hf)][2n, 2n + 1]
-    auto flush = [&](int u) {
-        if (u == cnt0 - 1 || u == total - 1)
+    // half-units [v0, v1) of the stream (v1 - v0 even); the first is already
+    // loaded into set A, and the one after the last is left loaded in set A
+    auto run = [&](int v0, int v1) {
+        for (int v = v0; v < v1; v += 2)
         {
-            const int i = u < cnt0 ? qa : pr;
+            DQ_LOAD(dsB, kkB, v + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            DQ_MFMA(dsA, kkA);
+            __builtin_amdgcn_sched_barrier(0);
+            DQ_LOAD(dsA, kkA, v + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            DQ_MFMA(dsB, kkB);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Partials: register r of lane (n, hf) holds dQ[32 i + row(r, hf)][2n, 2n + 1].
+    // Each wave parks its heavy-block partial in its LDS slot when it moves
+    // on to the light block (no barrier there), and the blocks are added
+    // over the 4 slots only at the end, in a fixed order: thread tid adds
+    // float4s tid, tid + 256 of the 32 x 64 block.
+    __shared__ __attribute__((aligned(16))) float red[4][32 * 64];
+    auto park = [&]() {
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
+        for (int r = 0; r < 16; ++r)
+            *reinterpret_cast<float2 *>(&red[w][mfma_row(r, hf) * 64 + 2 * n]) = make_float2(a0[r], a1[r]);
+    };
+    auto sum_store = [&](int i) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+        {
+            const int e = tid + 256 * k, row = 32 * i + (e >> 4);
+            float4 s = reinterpret_cast<const float4 *>(red[0])[e];
+#pragma unroll
+            for (int ww = 1; ww < 4; ++ww)
             {
-                const int row = 32 * i + mfma_row(r, hf);
-                if (row < T)
-                    *reinterpret_cast<float2 *>(gx + (long)row * 3 * C + 2 * n) =
-                        make_float2(a0[r] * scale, a1[r] * scale);
+                const float4 x = reinterpret_cast<const float4 *>(red[ww])[e];
+                s.x += x.x;
+                s.y += x.y;
+                s.z += x.z;
+                s.w += x.w;
             }
-            a0 = zero16();
-            a1 = zero16();
+            if (row < T)
+                *reinterpret_cast<float4 *>(gx + (long)row * 3 * C + 4 * (e & 15)) =
+                    make_float4(s.x * scale, s.y * scale, s.z * scale, s.w * scale);
         }
     };
 
     DQ_LOAD(dsA, kkA, 0);
-    for (int u = 0; u < total; u += 2)
+    __builtin_amdgcn_sched_barrier(0);
+    run(0, 2 * na);
+    park();
+    if (two)
     {
-        DQ_LOAD(dsB, kkB, u + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        DQ_MFMA(dsA, kkA);
-        __builtin_amdgcn_sched_barrier(0);
-        flush(u);
-        if (u + 1 >= total)
-            break;
-        DQ_LOAD(dsA, kkA, u + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        DQ_MFMA(dsB, kkB);
-        __builtin_amdgcn_sched_barrier(0);
-        flush(u + 1);
+        a0 = zero16();
+        a1 = zero16();
+        run(2 * na, 2 * nu);
+    }
+    __syncthreads();
+    sum_store(qa);
+    if (two)
+    {
+        __syncthreads();
+        park();
+        __syncthreads();
+        sum_store(pr);
     }
 #undef DQ_LOAD
 #undef DQ_MFMA
@@ -667,7 +710,7 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
                            grad_x, ws, lse, D, dy, qkv, s.T, s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale,
                            cu_count());
         timer_end(st);
-        const unsigned dq_blocks = (unsigned)((long)((n_qb + 1) / 2 + 3) / 4 * cnt);  // 4 pairs per workgroup
+        const unsigned dq_blocks = (unsigned)((long)((n_qb + 1) / 2) * cnt);  // one workgroup per pair
         timer_begin(kKindDq, st);
         hipLaunchKernelGGL(bwd_dq_d64_kernel, dim3(dq_blocks), dim3(256), 0, st, grad_x, ws, qkv, s.T, s.C, s.H,
                            bh0, cnt, n_qb, scale);

@@ -134,10 +134,21 @@ __device__ __forceinline__ void wave_lds_sync()
 // gfx9 word-3 for untyped 32-bit data). A load whose VGPR offset lies at or
 // past `bytes` returns zeros instead of touching memory, which is how the
 // kernels read rows past T: no clamps, no branches.
+// The base and size must be wave-uniform; they are passed through
+// readfirstlane so that the descriptor stays in SGPRs even where the compiler
+// has computed the address arithmetic in VGPRs (a descriptor it cannot prove
+// uniform turns every load into a waterfall loop).
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes)
 {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+    // (readfirstlane is int -> int: each half goes back through uint32_t, so
+    // that the low word is zero-extended, not sign-extended into the high word)
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    const uint64_t u = ((uint64_t)hi << 32) | (uint64_t)lo;
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(u), (short)0,
+                                             __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000);
 }
 // Buffer offset used for a block that does not exist: past the end of every
 // buffer range the kernels build (the host only takes the buffer-load kernels
