@@ -176,9 +176,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     float *ws = dsw + (long)bhl * ((long)n_qb * (n_qb + 1) / 2) * 1024;
     float *gx = grad_x + (long)b * T * 3L * C + (long)h * 64;
 
-    // Q, dO of the block, swizzled (tile_off)
-    __shared__ __attribute__((aligned(16))) float sq[2][32 * ST], so[2][32 * ST];
-    __shared__ __attribute__((aligned(16))) float sl[2][32], sd[2][32];             // lse * log2(e), D
+    // Q, dO of the block, swizzled (tile_off), and its lse (0..31) and D
+    // (64..95) rows; one array per buffer, so that the compiler sees that
+    // loads landing in one buffer do not alias reads of the other
+    __shared__ __attribute__((aligned(16))) float sq0[32 * ST], so0[32 * ST], sld0[128];
+    __shared__ __attribute__((aligned(16))) float sq1[32 * ST], so1[32 * ST], sld1[128];
+    auto bufs = [&](auto buf_c) {
+        constexpr int buf = decltype(buf_c)::value;
+        struct B
+        {
+            float *q, *o, *ld;
+        };
+        return buf == 0 ? B{sq0, so0, sld0} : B{sq1, so1, sld1};
+    };
 
     // stationary B operands: lane l holds K / V[kw0 + l%16][16 (l/16) + m],
     // m = 0..15 (MFMA m contracts d = m + 16 kk, kk = l/16)
@@ -201,60 +211,148 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
         }
     }
 
-    // staging: thread tid moves float4s tid + 256 u (u = 0, 1) of the Q and dO
-    // tiles (row = idx / 16, column 4 (idx % 16)); threads 0..31 an lse row,
-    // 32..63 a D row
-    constexpr int NT = 256, NU = 512 / NT;
-    const int r0 = tid >> 4, cc = tid & 15, t_st = tile_off(r0, cc);
-    const uint32_t st_q = (uint32_t)r0 * Wb + 16u * cc, st_o = (uint32_t)r0 * Cb + 16u * cc;
-    float4 pq[NU], po[NU];
-    float pld = 0.f;
-    auto issue = [&](int i) {
+    // Staging goes straight from memory into LDS (buffer loads to LDS, no
+    // registers). A 32 x 64 tile is 8 chunks of 1 KiB, chunk k = rows
+    // 4k .. 4k + 3; wave w moves chunks w and w + 4 of Q and of dO. Lane l
+    // lands at row 4k + l/16, physical column group l%16, so it fetches the
+    // logical group (l%16) ^ tile_swz(row), tile_swz(row) = (l/16) << 2 | w for
+    // both of its chunks. Wave 0 also moves the lse and D rows of the block.
+    const uint32_t dma_row = (uint32_t)(4 * w + (lane >> 4));
+    const uint32_t dma_col = 16u * (uint32_t)((lane & 15) ^ (((lane >> 4) << 2) | w));
+    const uint32_t dq_lane = dma_row * Wb + dma_col, do_lane = dma_row * Cb + dma_col;
+    // lse / D rows: lanes 0..31 fetch rows 0..31, lanes 32..63 land zeros
+    const uint32_t ld_lane = lane < 32 ? (uint32_t)lane * Hb : kNoBlock;
+    auto issue = [&](int i, auto buf_c) {
+        const auto B = bufs(buf_c);
         const bool ok = i < n_qb;
         const uint32_t qo = ok ? 32u * (uint32_t)i * Wb : kNoBlock, oo = ok ? 32u * (uint32_t)i * Cb : kNoBlock;
-#pragma unroll
-        for (int u = 0; u < NU; ++u)
+        dma16(rq, B.q + 256 * w, dq_lane, qo);
+        dma16(rq, B.q + 256 * (w + 4), dq_lane + 16u * Wb, qo);
+        dma16(ro, B.o + 256 * w, do_lane, oo);
+        dma16(ro, B.o + 256 * (w + 4), do_lane + 16u * Cb, oo);
+        if (w == 0)
         {
-            pq[u] = bload4s(rq, st_q + (uint32_t)(u * NT / 16) * Wb, qo);
-            po[u] = bload4s(ro, st_o + (uint32_t)(u * NT / 16) * Cb, oo);
+            const uint32_t lo = ok ? 32u * (uint32_t)i * Hb : kNoBlock;
+            dma4(rl, B.ld, ld_lane, lo);
+            dma4(rd, B.ld + 64, ld_lane, lo);
         }
-        const uint32_t lo = ok ? 32u * (uint32_t)i * Hb : kNoBlock;
-        if (tid < 32)
-            pld = bload1s(rl, (uint32_t)tid * Hb, lo) * kLog2e;
-        else if (tid < 64)
-            pld = bload1s(rd, (uint32_t)(tid - 32) * Hb, lo);
-    };
-    auto commit = [&](auto buf_c) {
-        constexpr int buf = decltype(buf_c)::value;
-#pragma unroll
-        for (int u = 0; u < NU; ++u)
-        {
-            *reinterpret_cast<float4 *>(&sq[buf][(u * NT / 16) * ST + t_st]) = pq[u];
-            *reinterpret_cast<float4 *>(&so[buf][(u * NT / 16) * ST + t_st]) = po[u];
-        }
-        if (tid < 32)
-            sl[buf][tid] = pld;
-        else if (tid < 64)
-            sd[buf][tid - 32] = pld;
     };
 
     v4f dk0 = zero4(), dk1 = zero4(), dk2 = zero4(), dk3 = zero4();
     v4f dv0 = zero4(), dv1 = zero4(), dv2 = zero4(), dv3 = zero4();
     const int i_lo = 2 * J;
-    issue(i_lo);
-    commit(BufIdx<0>{});
+    issue(i_lo, BufIdx<0>{});
+    lds_dma_wait();
     __syncthreads();
-    // one query block; the LDS buffer index is a compile-time constant (the
-    // loop below is unrolled by two) so that it folds into the ds_read offsets
-    auto step = [&](const int i, auto buf_c) {
+    // One query block; the LDS buffer index is a compile-time constant (the
+    // loop below is unrolled by two) so that it folds into the ds_read offsets.
+    // Only a workgroup's first two blocks (i = 2J, 2J + 1) can hold keys past
+    // queries, so only they (GEN) test for skipped tiles, zero halves and the
+    // causal mask; every later block is a full unmasked tile for every wave,
+    // a loop without branches (a branch around the dS stores would also make
+    // the compiler's waits for the staging loads pessimistic).
+    auto step = [&](const int i, auto buf_c, auto gen_c) {
         constexpr int buf = decltype(buf_c)::value;
-        issue(i + 1);
+        constexpr bool GEN = decltype(gen_c)::value;
+        issue(i + 1, BufIdx<buf ^ 1>{});
         __builtin_amdgcn_sched_barrier(0);
         const int q0 = 32 * i;
-        if (kw0 <= q0 + 31)  // else all 16 keys lie past this block's last query: no tile
+        const auto Bf = bufs(buf_c);
+        const float *Qs = Bf.q, *Os = Bf.o, *LDs = Bf.ld;
+        float *tile = ws + ds_tile(i, kw0 >> 5) + (kw0 & 31) + c16 + (4 * g4) * 32;
+        // Half t of the tile: queries q0 + 16 t .. + 15 against this wave's
+        // 16 keys, done start to end (S, dP, P, dS, its dS rows, dV and dK)
+        // before the other half, so only one half's accumulators are live.
+        auto half = [&](auto t_c) {
+            constexpr int t = decltype(t_c)::value;
+            // S[query q0 + 16t + 4 g4 + r][key kw0 + c16], dP likewise
+            v4f sa = zero4(), pa = zero4();
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+            {
+                const int ta = 16 * t * ST + tile_off(c16, 4 * g4 + c);
+                const float4 qa = *reinterpret_cast<const float4 *>(Qs + ta);
+                const float4 oa = *reinterpret_cast<const float4 *>(Os + ta);
+                const float qv[4] = {qa.x, qa.y, qa.z, qa.w}, ov[4] = {oa.x, oa.y, oa.z, oa.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                {
+                    sa = mfma16(qv[e], kreg[4 * c + e], sa);
+                    pa = mfma16(ov[e], vreg[4 * c + e], pa);
+                }
+            }
+            // P and dS (without the 1/sqrt(d)); zero where key > query. Rows
+            // past T need no mask: their Q, dO, lse and D load as zeros, so
+            // P = 1 and dS = 0 there and they add nothing to dK, dV or dQ.
+            {
+                const float4 L = *reinterpret_cast<const float4 *>(LDs + 16 * t + 4 * g4);
+                const float4 D = *reinterpret_cast<const float4 *>(LDs + 64 + 16 * t + 4 * g4);
+                const float lv[4] = {L.x * kLog2e, L.y * kLog2e, L.z * kLog2e, L.w * kLog2e};
+                const float dv[4] = {D.x, D.y, D.z, D.w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                {
+                    const float p = fast_exp2(fmaf(sa[r], c2, -lv[r]));
+                    sa[r] = p;
+                    pa[r] = p * (pa[r] - dv[r]);
+                }
+                if (GEN && q0 + 16 * t < kw0 + 15)  // some key of this wave lies past some query of the half
+                {
+                    const int key = kw0 + c16;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (key > q0 + 16 * t + 4 * g4 + r)
+                            sa[r] = pa[r] = 0.f;
+                }
+            }
+            // this wave's 16 x 16 quarter of dS tile (i, kw0 / 32), query-major
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                tile[(16 * t + r) * 32] = pa[r];
+            // dV += P^T dO, dK += dS^T Q: step r contracts queries
+            // q0 + 16t + 4kk + r (kk = l/16); B operands dO / Q[that query][4 c16 + e]
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+            {
+                const int tb = tile_off(16 * t + 4 * g4 + r, c16);
+                const float4 ob = *reinterpret_cast<const float4 *>(Os + tb);
+                const float4 qb = *reinterpret_cast<const float4 *>(Qs + tb);
+                dv0 = mfma16(sa[r], ob.x, dv0);
+                dv1 = mfma16(sa[r], ob.y, dv1);
+                dv2 = mfma16(sa[r], ob.z, dv2);
+                dv3 = mfma16(sa[r], ob.w, dv3);
+                dk0 = mfma16(pa[r], qb.x, dk0);
+                dk1 = mfma16(pa[r], qb.y, dk1);
+                dk2 = mfma16(pa[r], qb.z, dk2);
+                dk3 = mfma16(pa[r], qb.w, dk3);
+            }
+        };
+        // then wait until block i + 1 has landed in the other buffer: its
+        // loads were issued before this block's 8 dS stores, if any
+        if constexpr (GEN)
         {
-            const float *Qs = sq[buf], *Os = so[buf];
-            // S_t[query q0 + 16t + 4 g4 + r][key kw0 + c16], dP likewise
+            if (kw0 <= q0 + 31)  // else all 16 keys lie past this block's last query: no tile
+            {
+                if (kw0 < q0 + 16)
+                    half(BufIdx<0>{});
+                else  // kw0 = q0 + 16: every key lies past the first 16 queries, whose dS rows are zero
+                {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        tile[r * 32] = 0.f;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                half(BufIdx<1>{});
+                __builtin_amdgcn_sched_barrier(0);
+                vm_wait<8>();
+            }
+            else
+                lds_dma_wait();
+        }
+        else
+        {
+            // full unmasked tile, both halves at once (four independent
+            // S / dP accumulator chains)
             v4f s0 = zero4(), s1 = zero4(), p0 = zero4(), p1 = zero4();
 #pragma unroll
             for (int c = 0; c < 4; ++c)
@@ -275,15 +373,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                     p1 = mfma16(o1v[e], vreg[4 * c + e], p1);
                 }
             }
-            // P and dS (without the 1/sqrt(d)); zero where key > query. Rows
-            // past T need no mask: their Q, dO, lse and D load as zeros, so
-            // P = 1 and dS = 0 there and they add nothing to dK, dV or dQ.
             {
-                const float4 L0 = *reinterpret_cast<const float4 *>(&sl[buf][4 * g4]);
-                const float4 L1 = *reinterpret_cast<const float4 *>(&sl[buf][16 + 4 * g4]);
-                const float4 D0 = *reinterpret_cast<const float4 *>(&sd[buf][4 * g4]);
-                const float4 D1 = *reinterpret_cast<const float4 *>(&sd[buf][16 + 4 * g4]);
-                const float l0v[4] = {L0.x, L0.y, L0.z, L0.w}, l1v[4] = {L1.x, L1.y, L1.z, L1.w};
+                const float4 L0 = *reinterpret_cast<const float4 *>(LDs + 4 * g4);
+                const float4 L1 = *reinterpret_cast<const float4 *>(LDs + 16 + 4 * g4);
+                const float4 D0 = *reinterpret_cast<const float4 *>(LDs + 64 + 4 * g4);
+                const float4 D1 = *reinterpret_cast<const float4 *>(LDs + 80 + 4 * g4);
+                const float l0v[4] = {L0.x * kLog2e, L0.y * kLog2e, L0.z * kLog2e, L0.w * kLog2e};
+                const float l1v[4] = {L1.x * kLog2e, L1.y * kLog2e, L1.z * kLog2e, L1.w * kLog2e};
                 const float d0v[4] = {D0.x, D0.y, D0.z, D0.w}, d1v[4] = {D1.x, D1.y, D1.z, D1.w};
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
@@ -294,32 +390,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                     s1[r] = pb;
                     p1[r] = pb * (p1[r] - d1v[r]);
                 }
-                if (q0 < kw0 + 15)  // some key of this wave lies past some query of the block
-                {
-                    const int key = kw0 + c16;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                    {
-                        const int qa = q0 + 4 * g4 + r, qb = qa + 16;
-                        if (key > qa)
-                            s0[r] = p0[r] = 0.f;
-                        if (key > qb)
-                            s1[r] = p1[r] = 0.f;
-                    }
-                }
             }
-            // this wave's 32 x 16 half of dS tile (i, kw0 / 32), query-major
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
             {
-                float *tile = ws + ds_tile(i, kw0 >> 5) + (kw0 & 31) + c16 + (4 * g4) * 32;
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                {
-                    tile[r * 32] = p0[r];
-                    tile[(16 + r) * 32] = p1[r];
-                }
+                tile[r * 32] = p0[r];
+                tile[(16 + r) * 32] = p1[r];
             }
-            // dV += P^T dO, dK += dS^T Q: step (t, r) contracts queries
-            // q0 + 16t + 4kk + r (kk = l/16); B operands dO / Q[that query][4 c16 + e]
 #pragma unroll
             for (int t = 0; t < 2; ++t)
             {
@@ -340,19 +417,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                     dk3 = mfma16(ad, qb.w, dk3);
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
+            vm_wait<8>();
         }
-        __builtin_amdgcn_sched_barrier(0);
-        commit(BufIdx<buf ^ 1>{});
-        __syncthreads();
+        lds_barrier();
     };
-    int i = i_lo;
+    step(i_lo, BufIdx<0>{}, BufIdx<1>{});
+    if (i_lo + 1 < n_qb)
+        step(i_lo + 1, BufIdx<1>{}, BufIdx<1>{});
+    int i = i_lo + 2;
     for (; i + 1 < n_qb; i += 2)
     {
-        step(i, BufIdx<0>{});
-        step(i + 1, BufIdx<1>{});
+        step(i, BufIdx<0>{}, BufIdx<0>{});
+        step(i + 1, BufIdx<1>{}, BufIdx<0>{});
     }
     if (i < n_qb)
-        step(i, BufIdx<0>{});
+        step(i, BufIdx<0>{}, BufIdx<0>{});
 
     // register r of lane l: key kw0 + 4 g4 + r, dims 4 c16 + e (accumulator e)
 #pragma unroll

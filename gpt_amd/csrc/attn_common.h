@@ -172,6 +172,45 @@ __device__ __forceinline__ float bload1(rsrc_t r, uint32_t off)
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
 }
 
+// Loads straight into LDS (buffer_load ... lds): lane l's 4 or 16 bytes land
+// at lds + 4 l or lds + 16 l bytes (checked on gfx950; the global side may
+// be any per-lane offset). `lds` must be wave-uniform. The loads count in
+// vmcnt like any other; lds_dma_wait() waits for this wave's to land, and a
+// workgroup barrier after it makes them visible to the other waves. Offsets
+// past the buffer's range land as zeros, as for register loads.
+__device__ __forceinline__ void dma16(rsrc_t r, float *lds, uint32_t voff, uint32_t soff)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, (int)voff,
+                                             (int)soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(rsrc_t r, float *lds, uint32_t voff, uint32_t soff)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 4, (int)voff,
+                                             (int)soff, 0, 0);
+}
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left at their maxima; N < 16). On
+// gfx9 vector memory operations, loads and stores alike, retire in issue
+// order, so vmcnt(N) waits for everything but the N most recent ones: a wave
+// that issued N stores after its loads to LDS waits for those loads alone.
+template <int N>
+__device__ __forceinline__ void vm_wait()
+{
+    static_assert(N >= 0 && N < 16, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+__device__ __forceinline__ void lds_dma_wait() { vm_wait<0>(); }
+
+// Workgroup barrier that orders LDS only: unlike __syncthreads(), whose
+// fences also cover global memory and so wait for every outstanding global
+// store (vmcnt(0)), it waits for this wave's LDS operations alone. Loads to
+// LDS count in vmcnt and must be waited for (vm_wait) before it.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // The same loads with a wave-uniform part of the offset in an SGPR (soffset).
 // gfx950's range check applies to voffset + soffset + the immediate, so rows
 // past the range still read as zeros, and block / row bases cost no VGPRs.
