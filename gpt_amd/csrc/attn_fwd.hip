@@ -386,8 +386,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
                                 (uint32_t)(((long)T * 3 * C - (long)h * 64) * 4));
 
     // K tiles swizzled (tile_off), V tiles plain 64-word rows: the V reads
-    // (row 4 (l/16) + r, column group l%16) are conflict-free unswizzled
-    __shared__ __attribute__((aligned(16))) float sk[2][32 * ST], sv[2][32 * ST];
+    // (row 4 (l/16) + r, column group l%16) are conflict-free unswizzled. One
+    // array per buffer, so that the compiler sees that loads landing in one
+    // buffer do not alias reads of the other.
+    __shared__ __attribute__((aligned(16))) float sk0[32 * ST], sv0[32 * ST], sk1[32 * ST], sv1[32 * ST];
+    auto bufs = [&](auto buf_c) {
+        constexpr int buf = decltype(buf_c)::value;
+        struct B
+        {
+            float *k, *v;
+        };
+        return buf == 0 ? B{sk0, sv0} : B{sk1, sv1};
+    };
 
     // stationary B operand: lane l holds Q[qw0 + l%16][16 (l/16) + m], m = 0..15
     // (MFMA m contracts d = m + 16 kk, kk = l/16)
@@ -405,42 +415,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
         }
     }
 
-    // staging: thread tid moves float4s tid and tid + 256 of the K and V tiles
-    // (row = idx / 16, column 4 (idx % 16))
-    const int r0 = tid >> 4, cc = tid & 15, k_st = tile_off(r0, cc);
-    const uint32_t st_k = (uint32_t)r0 * Wb + Cb + 16u * cc;
-    float4 pk[2], pv[2];
+    // Staging goes straight from memory into LDS (buffer loads to LDS, no
+    // registers). A 32 x 64 tile is 8 chunks of 1 KiB, chunk k = rows
+    // 4k .. 4k + 3; wave w moves chunks w and w + 4 of the K and of the V
+    // tile. Lane l lands at row 4k + l/16, physical column group l%16: for the
+    // swizzled K tile it fetches the logical group (l%16) ^ tile_swz(row),
+    // tile_swz(row) = (l/16) << 2 | w for both of its chunks.
+    const uint32_t dma_row = (uint32_t)(4 * w + (lane >> 4));
+    const uint32_t k_lane = dma_row * Wb + Cb + 16u * (uint32_t)((lane & 15) ^ (((lane >> 4) << 2) | w));
+    const uint32_t v_lane = dma_row * Wb + 2u * Cb + 16u * (uint32_t)(lane & 15);
     const int kb_end = min(2 * J + 2, (T + 31) / 32);  // key blocks 0 .. kb_end - 1
-    auto issue = [&](int kb) {
+    auto issue = [&](int kb, auto buf_c) {
+        const auto B = bufs(buf_c);
         const uint32_t ko = kb < kb_end ? 32u * (uint32_t)kb * Wb : kNoBlock;
-        pk[0] = bload4s(rs, st_k, ko);
-        pk[1] = bload4s(rs, st_k + 16u * Wb, ko);
-        pv[0] = bload4s(rs, st_k + Cb, ko);
-        pv[1] = bload4s(rs, st_k + Cb + 16u * Wb, ko);
-    };
-    auto commit = [&](int buf) {
-        *reinterpret_cast<float4 *>(&sk[buf][k_st]) = pk[0];
-        *reinterpret_cast<float4 *>(&sk[buf][16 * ST + k_st]) = pk[1];
-        *reinterpret_cast<float4 *>(&sv[buf][r0 * ST + 4 * cc]) = pv[0];
-        *reinterpret_cast<float4 *>(&sv[buf][(r0 + 16) * ST + 4 * cc]) = pv[1];
+        dma16(rs, B.k + 256 * w, k_lane, ko);
+        dma16(rs, B.k + 256 * (w + 4), k_lane + 16u * Wb, ko);
+        dma16(rs, B.v + 256 * w, v_lane, ko);
+        dma16(rs, B.v + 256 * (w + 4), v_lane + 16u * Wb, ko);
     };
 
     v4f o0 = zero4(), o1 = zero4(), o2 = zero4(), o3 = zero4();  // O^T, d = 16 g4 + 4 r + e
     // reference max (log2 units, the same in the 4 lane groups of a query) of
     // query qw0 + c16 and this lane's part of its row sum
     float m = -INFINITY, l = 0.f;
-    issue(0);
-    commit(0);
-    __syncthreads();
-    for (int kb = 0; kb < kb_end; ++kb)
-    {
-        const int buf = kb & 1;
-        issue(kb + 1);
+
+    // One key block, in LDS buffer buf (a compile-time constant, so that it
+    // folds into the ds_read offsets). Only the last two blocks (2J, 2J + 1)
+    // can hold keys past queries; only they (GEN) test for a skipped block,
+    // a fully masked second 16-key half (HALF: k0 = qw0) and the causal mask.
+    auto block = [&](const int kb, auto buf_c, auto gen_c) {
+        constexpr int buf = decltype(buf_c)::value;
+        constexpr bool GEN = decltype(gen_c)::value;
+        issue(kb + 1, BufIdx<buf ^ 1>{});
         __builtin_amdgcn_sched_barrier(0);
         const int k0 = 32 * kb;
-        if (k0 <= qw0 + 15)  // else every key of the block lies past this wave's queries
-        {
-            const float *Ks = sk[buf], *Vs = sv[buf];
+        const auto B = bufs(buf_c);
+        const float *Ks = B.k, *Vs = B.v;
+        auto tile = [&](auto half_c) {
+            constexpr bool HALF = decltype(half_c)::value;
             // S^T_kt[key k0 + 16 kt + 4 g4 + r][query qw0 + c16] (unscaled)
             v4f s0 = zero4(), s1 = zero4();
 #pragma unroll
@@ -448,16 +460,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
             {
                 const int ko = tile_off(c16, 4 * g4 + c);
                 const float4 ka = *reinterpret_cast<const float4 *>(Ks + ko);
-                const float4 kb4 = *reinterpret_cast<const float4 *>(Ks + 16 * ST + ko);
-                const float kav[4] = {ka.x, ka.y, ka.z, ka.w}, kbv[4] = {kb4.x, kb4.y, kb4.z, kb4.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
+                const float kav[4] = {ka.x, ka.y, ka.z, ka.w};
+                if constexpr (!HALF)
                 {
-                    s0 = mfma16(kav[e], qreg[4 * c + e], s0);
-                    s1 = mfma16(kbv[e], qreg[4 * c + e], s1);
+                    const float4 kb4 = *reinterpret_cast<const float4 *>(Ks + 16 * ST + ko);
+                    const float kbv[4] = {kb4.x, kb4.y, kb4.z, kb4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                    {
+                        s0 = mfma16(kav[e], qreg[4 * c + e], s0);
+                        s1 = mfma16(kbv[e], qreg[4 * c + e], s1);
+                    }
+                }
+                else
+                {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        s0 = mfma16(kav[e], qreg[4 * c + e], s0);
                 }
             }
-            if (k0 + 31 > qw0)
+            if (GEN && k0 + 31 > qw0)
             {
                 // diagonal block: key > query is masked out
                 const int q = qw0 + c16;
@@ -466,7 +488,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
                 {
                     if (k0 + 4 * g4 + r > q)
                         s0[r] = -INFINITY;
-                    if (k0 + 16 + 4 * g4 + r > q)
+                    if (HALF || k0 + 16 + 4 * g4 + r > q)
                         s1[r] = -INFINITY;
                 }
             }
@@ -517,20 +539,58 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
             for (int r = 0; r < 4; ++r)
             {
                 const float4 va = *reinterpret_cast<const float4 *>(Vs + (4 * g4 + r) * ST + 4 * c16);
-                const float4 vb = *reinterpret_cast<const float4 *>(Vs + (16 + 4 * g4 + r) * ST + 4 * c16);
                 o0 = mfma16(va.x, s0[r], o0);
                 o1 = mfma16(va.y, s0[r], o1);
                 o2 = mfma16(va.z, s0[r], o2);
                 o3 = mfma16(va.w, s0[r], o3);
-                o0 = mfma16(vb.x, s1[r], o0);
-                o1 = mfma16(vb.y, s1[r], o1);
-                o2 = mfma16(vb.z, s1[r], o2);
-                o3 = mfma16(vb.w, s1[r], o3);
+                if constexpr (!HALF)
+                {
+                    const float4 vb = *reinterpret_cast<const float4 *>(Vs + (16 + 4 * g4 + r) * ST + 4 * c16);
+                    o0 = mfma16(vb.x, s1[r], o0);
+                    o1 = mfma16(vb.y, s1[r], o1);
+                    o2 = mfma16(vb.z, s1[r], o2);
+                    o3 = mfma16(vb.w, s1[r], o3);
+                }
             }
+        };
+        if constexpr (GEN)
+        {
+            if (k0 == qw0)
+                tile(BufIdx<1>{});
+            else if (k0 <= qw0 + 15)  // else every key of the block lies past this wave's queries
+                tile(BufIdx<0>{});
         }
+        else
+            tile(BufIdx<0>{});
         __builtin_amdgcn_sched_barrier(0);
-        commit(buf ^ 1);
-        __syncthreads();
+        lds_dma_wait();  // block kb + 1 has landed in the other buffer
+        lds_barrier();
+    };
+
+    issue(0, BufIdx<0>{});
+    lds_dma_wait();
+    lds_barrier();
+    // blocks 0 .. kb_end - 3 lie wholly before this workgroup's queries
+    const int kb_gen = kb_end > 2 ? kb_end - 2 : 0;
+    int kb = 0;
+    for (; kb + 1 < kb_gen; kb += 2)
+    {
+        block(kb, BufIdx<0>{}, BufIdx<0>{});
+        block(kb + 1, BufIdx<1>{}, BufIdx<0>{});
+    }
+    if (kb < kb_gen)  // odd count: one more plain block, the others start in buffer 1
+    {
+        block(kb, BufIdx<0>{}, BufIdx<0>{});
+        block(kb + 1, BufIdx<1>{}, BufIdx<1>{});
+        if (kb + 2 < kb_end)
+            block(kb + 2, BufIdx<0>{}, BufIdx<1>{});
+    }
+    else
+    {
+        if (kb < kb_end)
+            block(kb, BufIdx<0>{}, BufIdx<1>{});
+        if (kb + 1 < kb_end)
+            block(kb + 1, BufIdx<1>{}, BufIdx<1>{});
     }
 
     // register r of accumulator e: O[qw0 + c16][16 g4 + 4 r + e]
