@@ -7,7 +7,10 @@
 // and replacing the reference's CUDA kernel (src/backend/cuda/kernels/
 // attention.cu:6-268).
 //
-// head_dim 64 kernel (fwd_d64_kernel). Work unit = one 32-query block x one
+// head_dim 64 kernels. fwd_qs_d64_kernel (below) for calls with at least 256
+// 64-query groups, fwd_split_d64_kernel (below) for very small calls, and:
+//
+// fwd_d64_kernel (the calls in between). Work unit = one 32-query block x one
 // 32-key block of the causal triangle; query block i has i + 1 units. Each
 // workgroup takes a heavy/light pair of query blocks (n - 1 - p, p) of one
 // (b, h), i.e. n + 1 units for n query blocks, so every workgroup carries the
@@ -609,6 +612,202 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
     }
 }
 
+// Split-key head_dim-64 forward for calls too small to fill the GPU with
+// 64-query groups (fwd_split_d64_kernel: B = 1 generation prefixes, C1). One
+// workgroup per (b, h, 16-query group g), heaviest groups first; its NW waves
+// take the group's 32-key blocks round-robin (one block each up to T = 16 NW
+// ... 32 NW), so a call's latency is about one block instead of the whole
+// row. Each wave keeps the group's Q in registers (the MFMA B operand, as in
+// the Q-stationary kernel), loads its K and V blocks straight from memory as
+// MFMA operands, and runs the same S^T / online-softmax / O^T += V^T P^T steps
+// on v_mfma_f32_16x16x4_f32. The waves' partials (row max m, row sum l, O)
+// then meet in LDS: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w with
+// M = max_w m_w, in wave order.
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void fwd_split_d64_kernel(float *__restrict__ y, float *__restrict__ lse,
+                                                                const float *__restrict__ qkv, int T, int C, int H,
+                                                                int BH, int n_g, float c2)
+{
+    const int tid = threadIdx.x, lane = tid & 63, w = NW > 1 ? wave_id() : 0;
+    const int c16 = lane & 15, g4 = lane >> 4;
+    const int g = n_g - 1 - (int)(blockIdx.x / BH);
+    const int bh = (int)(blockIdx.x % BH), b = bh / H, h = bh % H;
+    const int q0 = 16 * g;
+    const int n_kb = (q0 + 15) / 32 + 1;  // key blocks 0 .. n_kb - 1 hold the keys <= q0 + 15
+    const uint32_t Wb = 12u * (uint32_t)C, Cb = 4u * (uint32_t)C;
+    const rsrc_t rs = make_rsrc(qkv + (long)b * T * 3L * C + (long)h * 64,
+                                (uint32_t)(((long)T * 3 * C - (long)h * 64) * 4));
+
+    // B operand: lane l holds Q[q0 + l%16][16 (l/16) + m], m = 0..15
+    float qreg[16];
+    {
+        const uint32_t off = (uint32_t)c16 * Wb + 64u * g4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+        {
+            const float4 q4 = bload4s(rs, off + 16u * c, (uint32_t)q0 * Wb);
+            qreg[4 * c + 0] = q4.x;
+            qreg[4 * c + 1] = q4.y;
+            qreg[4 * c + 2] = q4.z;
+            qreg[4 * c + 3] = q4.w;
+        }
+    }
+    // lane parts of a block's operand offsets: K[c16 (+16)][16 g4 + 4c ..],
+    // V[4 g4 + r (+16)][4 c16 ..]
+    const uint32_t k_lane = (uint32_t)c16 * Wb + Cb + 64u * g4;
+    const uint32_t v_lane = 4u * g4 * Wb + 2u * Cb + 16u * c16;
+
+    v4f o0 = zero4(), o1 = zero4(), o2 = zero4(), o3 = zero4();  // O^T, d = 16 g4 + 4 r + e
+    float m = -INFINITY, l = 0.f;  // max (log2 units) of query q0 + c16, this lane's part of its sum
+    for (int kb = w; kb < n_kb; kb += NW)
+    {
+        const int k0 = 32 * kb;
+        const uint32_t ko = (uint32_t)k0 * Wb;
+        float4 ka[4], kb4[4], va[4], vb[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+        {
+            ka[c] = bload4s(rs, k_lane + 16u * c, ko);
+            kb4[c] = bload4s(rs, k_lane + 16u * c + 16u * Wb, ko);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+        {
+            va[r] = bload4s(rs, v_lane + (uint32_t)r * Wb, ko);
+            vb[r] = bload4s(rs, v_lane + (uint32_t)(16 + r) * Wb, ko);
+        }
+        // S^T_kt[key k0 + 16 kt + 4 g4 + r][query q0 + c16] (unscaled)
+        v4f s0 = zero4(), s1 = zero4();
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+        {
+            const float kav[4] = {ka[c].x, ka[c].y, ka[c].z, ka[c].w};
+            const float kbv[4] = {kb4[c].x, kb4[c].y, kb4[c].z, kb4[c].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+            {
+                s0 = mfma16(kav[e], qreg[4 * c + e], s0);
+                s1 = mfma16(kbv[e], qreg[4 * c + e], s1);
+            }
+        }
+        if (k0 + 31 > q0)
+        {
+            // diagonal block: key > query is masked out
+            const int q = q0 + c16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+            {
+                if (k0 + 4 * g4 + r > q)
+                    s0[r] = -INFINITY;
+                if (k0 + 16 + 4 * g4 + r > q)
+                    s1[r] = -INFINITY;
+            }
+        }
+        // online softmax over this wave's blocks; its first block holds an
+        // unmasked key for every query (block w <= the diagonal), so m is
+        // finite from then on
+        float mt = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                         fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+        mt = halves_max(rows16_max(mt));
+        const float mn = fmaxf(m, mt * c2);
+        const float corr = fast_exp2(m - mn);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+        {
+            s0[r] = fast_exp2(fmaf(s0[r], c2, -mn));
+            s1[r] = fast_exp2(fmaf(s1[r], c2, -mn));
+        }
+        l = l * corr + (((s0[0] + s1[0]) + (s0[1] + s1[1])) + ((s0[2] + s1[2]) + (s0[3] + s1[3])));
+        m = mn;
+        o0 *= corr;
+        o1 *= corr;
+        o2 *= corr;
+        o3 *= corr;
+        // O^T += V^T P^T: step (kt, r) contracts keys k0 + 16 kt + 4 kk + r (kk = l/16)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+        {
+            o0 = mfma16(va[r].x, s0[r], o0);
+            o1 = mfma16(va[r].y, s0[r], o1);
+            o2 = mfma16(va[r].z, s0[r], o2);
+            o3 = mfma16(va[r].w, s0[r], o3);
+            o0 = mfma16(vb[r].x, s1[r], o0);
+            o1 = mfma16(vb[r].y, s1[r], o1);
+            o2 = mfma16(vb[r].z, s1[r], o2);
+            o3 = mfma16(vb[r].w, s1[r], o3);
+        }
+    }
+    l = halves_sum(rows16_sum(l));
+
+    const int row_base = q0;
+    if constexpr (NW == 1)
+    {
+        const int row = row_base + c16;
+        if (row < T)
+        {
+            const float inv = 1.f / l;
+            float *dst = y + ((long)b * T + row) * C + (long)h * 64 + 16 * g4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                *reinterpret_cast<float4 *>(dst + 4 * r) =
+                    make_float4(o0[r] * inv, o1[r] * inv, o2[r] * inv, o3[r] * inv);
+            if (g4 == 0)
+                lse[((long)b * T + row) * H + h] = (m + fast_log2(l)) * kLn2;
+        }
+    }
+    else
+    {
+        // partials to LDS (a wave without blocks contributes m = -inf, l = 0, O = 0)
+        __shared__ __attribute__((aligned(16))) float sm_o[NW][16 * 64];
+        __shared__ float sm_m[NW][16], sm_l[NW][16];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            *reinterpret_cast<float4 *>(&sm_o[w][c16 * 64 + 16 * g4 + 4 * r]) = make_float4(o0[r], o1[r], o2[r], o3[r]);
+        if (g4 == 0)
+        {
+            sm_m[w][c16] = m;
+            sm_l[w][c16] = l;
+        }
+        __syncthreads();
+        // thread tid: query row tid / (NW * 4), float4 columns strided by NW * 4
+        constexpr int TPR = NW * 4;  // threads per row
+        const int q = tid / TPR, part = tid % TPR;
+        float M = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww)
+            M = fmaxf(M, sm_m[ww][q]);
+        float L = 0.f, f[NW];
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww)
+        {
+            f[ww] = fast_exp2(sm_m[ww][q] - M);
+            L += f[ww] * sm_l[ww][q];
+        }
+        const float inv = 1.f / L;
+        const int row = row_base + q;
+        if (row < T)
+        {
+            float *dst = y + ((long)b * T + row) * C + (long)h * 64;
+            for (int c4 = part; c4 < 16; c4 += TPR)
+            {
+                float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int ww = 0; ww < NW; ++ww)
+                {
+                    const float4 x = *reinterpret_cast<const float4 *>(&sm_o[ww][q * 64 + 4 * c4]);
+                    acc.x += f[ww] * x.x;
+                    acc.y += f[ww] * x.y;
+                    acc.z += f[ww] * x.z;
+                    acc.w += f[ww] * x.w;
+                }
+                *reinterpret_cast<float4 *>(dst + 4 * c4) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+            }
+            if (part == 0)
+                lse[((long)b * T + row) * H + h] = (M + fast_log2(L)) * kLn2;
+        }
+    }
+}
+
 // General head_dim (1..DM): one thread per (b, h, query row), online softmax
 // over keys 0..i, q and the output row in registers.
 template <int DM>
@@ -703,6 +902,38 @@ hipError_t launch_fwd_d64(float *y, float *lse, const float *qkv, const Shape &s
         // enough 64-query groups to fill the GPU: the Q-stationary kernel
         hipLaunchKernelGGL(fwd_qs_d64_kernel, dim3((unsigned)((long)n_qg * BH)), dim3(256), 0, st, y, lse, qkv, s.T,
                            s.C, s.H, BH, n_qg, c2, fwd_cu_count());
+        timer_end(st);
+        return hipGetLastError();
+    }
+    const int n_g = (s.T + 15) / 16;
+    if ((long)n_g * BH <= 512)
+    {
+        // very small call (at most 2 workgroups per CU): the split-key kernel,
+        // one workgroup per 16-query group, up to 8 waves splitting its key
+        // blocks (one block each up to T = 256). Measured faster than the pair
+        // kernel up to this size (B=1 T=256: 9.6 vs 15.0 us; B=1 T=512: 15.5
+        // vs 19.8 us; B=2 T=256: 11.7 vs 15.4 us), slower past it (B=2 T=512:
+        // 22.3 vs 20.8 us; B=1 T=1024: 31.6 vs 30.3 us).
+        const int kb_max = (16 * (n_g - 1) + 15) / 32 + 1;
+        int sw = 1;
+        while (sw < kb_max && sw < 8)
+            sw <<= 1;
+        const dim3 g2((unsigned)((long)n_g * BH));
+        switch (sw)
+        {
+        case 8:
+            hipLaunchKernelGGL(fwd_split_d64_kernel<8>, g2, dim3(512), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_g, c2);
+            break;
+        case 4:
+            hipLaunchKernelGGL(fwd_split_d64_kernel<4>, g2, dim3(256), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_g, c2);
+            break;
+        case 2:
+            hipLaunchKernelGGL(fwd_split_d64_kernel<2>, g2, dim3(128), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_g, c2);
+            break;
+        default:
+            hipLaunchKernelGGL(fwd_split_d64_kernel<1>, g2, dim3(64), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_g, c2);
+            break;
+        }
         timer_end(st);
         return hipGetLastError();
     }
