@@ -92,8 +92,10 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(float *__restrict__ grad_
 }
 
 // D rows for head_dim 64: one wave per token row (all H heads), lane l reads
-// float4s l, l + 64, ... of the row; the 16 lanes of one head sum their
-// products in 4 butterfly steps.
+// float4s l, l + 64, ... of the row; the 16 lanes of one head (one DPP row)
+// sum their products with 4 DPP adds. The loads of up to 4 float4 pairs per lane
+// are all issued before the first sum, so a wave has one memory round trip
+// per 4 heads' worth of row instead of one per 64 lanes' worth.
 __global__ __launch_bounds__(256) void bwd_rowdot_d64_kernel(float *__restrict__ Dout,
                                                              const float *__restrict__ dy,
                                                              const float *__restrict__ y,
@@ -106,16 +108,32 @@ __global__ __launch_bounds__(256) void bwd_rowdot_d64_kernel(float *__restrict__
     const long C = 64L * H;
     const float4 *a = reinterpret_cast<const float4 *>(dy + row * C);
     const float4 *o = reinterpret_cast<const float4 *>(y + row * C);
-    for (int f = lane; f < 16 * H; f += 64)  // uniform within each 16-lane group
+    const int n4 = 16 * H;
+    for (int f0 = 0; f0 < n4; f0 += 256)
     {
-        const float4 u = a[f], v = o[f];
-        float s = u.x * v.x + u.y * v.y + u.z * v.z + u.w * v.w;
-        s += __shfl_xor(s, 8, 16);
-        s += __shfl_xor(s, 4, 16);
-        s += __shfl_xor(s, 2, 16);
-        s += __shfl_xor(s, 1, 16);
-        if ((lane & 15) == 0)
-            Dout[row * H + (f >> 4)] = s;
+        float4 u[4], v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            const int f = f0 + 64 * k + lane;
+            if (f < n4)  // uniform within each 16-lane group
+            {
+                u[k] = a[f];
+                v[k] = o[f];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            const int f = f0 + 64 * k + lane;
+            if (f < n4)
+            {
+                const float s =
+                    row16_sum(u[k].x * v[k].x + u[k].y * v[k].y + u[k].z * v[k].z + u[k].w * v[k].w);
+                if ((lane & 15) == 0)
+                    Dout[row * H + (f >> 4)] = s;
+            }
+        }
     }
 }
 

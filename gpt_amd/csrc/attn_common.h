@@ -121,6 +121,30 @@ __device__ __forceinline__ float rows16_sum(float x)
     return p.x + p.y;
 }
 
+// x of another lane of the same 16-lane DPP row (CTRL: a gfx9 DPP control,
+// e.g. 0x140 row_mirror: lane 15 - i; 0x141 row_half_mirror: lane 7 - i within
+// each 8-lane half; 0x4E quad_perm [2,3,0,1]: lane i ^ 2; 0xB1 quad_perm
+// [1,0,3,2]: lane i ^ 1). A VALU op, unlike the LDS bpermute of __shfl_xor.
+template <int CTRL> __device__ __forceinline__ float dpp_row(float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum of x over the 16 lanes of the DPP row, in every lane of the row (the
+// lanes add in different orders, so they may differ in the last bits; each
+// lane's result is the same from run to run). After the two mirrors lanes
+// 0..3 hold the sums of {0,15,7,8}, {1,14,6,9}, {2,13,5,10}, {3,12,4,11}
+// (lanes 4..7 the same groups in reverse, the upper half likewise), which
+// the two quad permutations add up.
+__device__ __forceinline__ float row16_sum(float x)
+{
+    x += dpp_row<0x140>(x);
+    x += dpp_row<0x141>(x);
+    x += dpp_row<0x4E>(x);
+    x += dpp_row<0xB1>(x);
+    return x;
+}
+
 // Compiler-level ordering point between one wave's LDS writes and its reads
 // of other lanes' values (a wave's LDS instructions execute in issue order).
 __device__ __forceinline__ void wave_lds_sync()

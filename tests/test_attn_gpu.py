@@ -128,6 +128,19 @@ def test_forward_kernel_choice(dev, B, T):
     check_fwd_bwd(dev, x, g, H, tag=f"B={B} T={T}")
 
 
+@pytest.mark.parametrize("B,T,H", [(2, 96, 1), (2, 70, 20), (1, 64, 33), (4, 256, 20), (2, 256, 33)])
+def test_head_counts_d64(dev, B, T, H):
+    """head_dim 64 with 1, 20 and 33 heads (C = 64, 1280, 2112): the
+    per-(b, h) index math of every kernel away from H = 12 (the last two
+    shapes take the Q-stationary forward, B*H = 66 not a multiple of 8), and
+    the D-row kernel's rows of more than 256 float4s (it takes a row in
+    chunks of 4 x 64 float4s)."""
+    C = 64 * H
+    x = synth.qkv(B, T, C, seed=7000 + H)
+    g = synth.grad_out(B, T, C, seed=7000 + H, std=1.0)
+    check_fwd_bwd(dev, x, g, H, tag=f"H={H}")
+
+
 def test_config5b_prefix_sweep_T1_to_256(dev):
     """Forward at B=1 for every prefix length 1..256, as autoregressive
     generation without a KV cache does."""
