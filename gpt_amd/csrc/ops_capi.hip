@@ -1,0 +1,488 @@
+// C ABI of the gfx950 GPT-2 ops around the attention path (declared in
+// include/gpt_hip_ops.h): argument validation, rocBLAS GEMMs for the matrix
+// products, launches of the element-wise / normalisation / reduction kernels
+// (ops_kernels.hip), status codes.
+//
+// The reference's op methods return void and abort on any runtime error
+// (src/backend/cuda/utils/cuda_utils.cuh:21-34); here every entry point returns
+// a status and keeps a per-thread message.
+#include "../../include/gpt_hip_ops.h"
+#include "ops_internal.h"
+
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <math.h>
+#include <mutex>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_device(const char *op)
+{
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0)
+        return fail(GPT_HIP_OPS_ENODEV, "%s: no HIP device (%s)", op,
+                    e != hipSuccess ? hipGetErrorString(e) : "device count is 0");
+    return 0;
+}
+
+int launched(const char *op, hipError_t e)
+{
+    if (e != hipSuccess)
+        return fail(GPT_HIP_OPS_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
+    return 0;
+}
+
+// Rows (B * T) of a [B, T, n] tensor, validated: non-negative, grid- and
+// index-sized (rows < 2^31, rows * n < 2^40).
+int check_rows(const char *op, int B, int T, long long n, long *rows)
+{
+    if (B < 0 || T < 0 || n <= 0)
+        return fail(GPT_HIP_OPS_EINVAL, "%s: invalid shape B=%d T=%d width=%lld", op, B, T, n);
+    const long long r = (long long)B * T;
+    if (r >= (1LL << 31) || r * n >= (1LL << 40))
+        return fail(GPT_HIP_OPS_ERANGE, "%s: tensor too large (B=%d T=%d width=%lld)", op, B, T, n);
+    *rows = (long)r;
+    return 0;
+}
+
+// ---------------------------------------------------------------- rocBLAS
+
+constexpr int kMaxDevices = 64;
+std::mutex g_blas_mu;
+rocblas_handle g_blas[kMaxDevices] = {};
+
+// One rocBLAS handle per device, created on first use with that device
+// current; atomics are disallowed so that every GEMM is deterministic.
+int blas_for(const char *op, hipStream_t st, rocblas_handle *out)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return fail(GPT_HIP_OPS_ENODEV, "%s: no current HIP device", op);
+    std::lock_guard<std::mutex> lock(g_blas_mu);
+    if (!g_blas[dev])
+    {
+        rocblas_handle h = nullptr;
+        if (rocblas_create_handle(&h) != rocblas_status_success)
+            return fail(GPT_HIP_OPS_ELAUNCH, "%s: rocblas_create_handle failed", op);
+        if (rocblas_set_atomics_mode(h, rocblas_atomics_not_allowed) != rocblas_status_success)
+            return fail(GPT_HIP_OPS_ELAUNCH, "%s: rocblas_set_atomics_mode failed", op);
+        g_blas[dev] = h;
+    }
+    if (rocblas_set_stream(g_blas[dev], st) != rocblas_status_success)
+        return fail(GPT_HIP_OPS_ELAUNCH, "%s: rocblas_set_stream failed", op);
+    *out = g_blas[dev];
+    return 0;
+}
+
+// Row-major C[M x N] = alpha op(A) op(B) + beta C, op(A) [M x K], op(B)
+// [K x N], leading dimensions in elements of the row-major storage. rocBLAS
+// is column-major: the row-major product is the column-major C^T = op(B)^T
+// op(A)^T, i.e. the same call with the operands swapped.
+int gemm_rm(const char *op, rocblas_handle h, bool ta, bool tb, int M, int N, int K, float alpha, const float *A,
+            int lda, const float *B, int ldb, float beta, float *C, int ldc)
+{
+    const rocblas_status s =
+        rocblas_sgemm(h, tb ? rocblas_operation_transpose : rocblas_operation_none,
+                      ta ? rocblas_operation_transpose : rocblas_operation_none, N, M, K, &alpha, B, ldb, A, lda,
+                      &beta, C, ldc);
+    if (s != rocblas_status_success)
+        return fail(GPT_HIP_OPS_ELAUNCH, "%s: rocblas_sgemm failed: %s", op, rocblas_status_to_string(s));
+    return 0;
+}
+
+// ---------------------------------------------------------------- workspace
+
+std::mutex g_pool_mu;
+bool g_pool_ready[kMaxDevices] = {};
+
+// Stream-ordered workspace from the device's default memory pool, told once
+// per device to keep freed memory, so steady-state calls do not allocate.
+int ws_alloc(const char *op, float **p, size_t floats, hipStream_t st)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return fail(GPT_HIP_OPS_ENODEV, "%s: no current HIP device", op);
+    {
+        std::lock_guard<std::mutex> lock(g_pool_mu);
+        if (!g_pool_ready[dev])
+        {
+            hipMemPool_t pool;
+            uint64_t keep = UINT64_MAX;
+            if (hipDeviceGetDefaultMemPool(&pool, dev) != hipSuccess ||
+                hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep) != hipSuccess)
+                return fail(GPT_HIP_OPS_ENOMEM, "%s: default memory pool unavailable", op);
+            g_pool_ready[dev] = true;
+        }
+    }
+    void *q = nullptr;
+    const hipError_t e = hipMallocAsync(&q, floats * sizeof(float), st);
+    if (e != hipSuccess)
+        return fail(GPT_HIP_OPS_ENOMEM, "%s: workspace of %zu bytes: %s", op, floats * sizeof(float),
+                    hipGetErrorString(e));
+    *p = static_cast<float *>(q);
+    return 0;
+}
+
+int ws_free(const char *op, float *p, hipStream_t st)
+{
+    const hipError_t e = hipFreeAsync(p, st);
+    if (e != hipSuccess)
+        return fail(GPT_HIP_OPS_ELAUNCH, "%s: workspace release failed: %s", op, hipGetErrorString(e));
+    return 0;
+}
+
+hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+int gpt_hip_embedding_forward_f32(float *y, const float *wte, const float *wpe, const int *input_tokens,
+                                  int batch_size, int seq_len, int hidden_size, int vocab_rows, void *stream)
+{
+    static const char *op = "gpt_hip_embedding_forward_f32";
+    long rows = 0;
+    if (int rc = check_rows(op, batch_size, seq_len, hidden_size, &rows))
+        return rc;
+    if (rows == 0)
+        return 0;
+    if (!y || !wte || !wpe || !input_tokens)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    return launched(op, gpt_ops::launch_embedding_fwd(y, wte, wpe, input_tokens, batch_size, seq_len, hidden_size,
+                                                      vocab_rows, as_stream(stream)));
+}
+
+int gpt_hip_embedding_backward_f32(float *grad_wte, float *grad_wpe, const float *grad_y, const int *input_tokens,
+                                   int batch_size, int seq_len, int hidden_size, int vocab_rows, void *stream)
+{
+    static const char *op = "gpt_hip_embedding_backward_f32";
+    long rows = 0;
+    if (int rc = check_rows(op, batch_size, seq_len, hidden_size, &rows))
+        return rc;
+    if (rows == 0)
+        return 0;
+    if (!grad_wte || !grad_wpe || !grad_y || !input_tokens)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    return launched(op, gpt_ops::launch_embedding_bwd(grad_wte, grad_wpe, grad_y, input_tokens, batch_size, seq_len,
+                                                      hidden_size, vocab_rows, as_stream(stream)));
+}
+
+int gpt_hip_unembedding_forward_f32(float *y, const float *x, const float *wte, int batch_size, int seq_len,
+                                    int hidden_size, int vocab_size_padded, void *stream)
+{
+    static const char *op = "gpt_hip_unembedding_forward_f32";
+    long rows = 0;
+    if (int rc = check_rows(op, batch_size, seq_len, (long long)hidden_size + vocab_size_padded, &rows))
+        return rc;
+    if (hidden_size <= 0 || vocab_size_padded <= 0)
+        return fail(GPT_HIP_OPS_EINVAL, "%s: hidden_size %d, vocab_size_padded %d", op, hidden_size,
+                    vocab_size_padded);
+    if (rows == 0)
+        return 0;
+    if (!y || !x || !wte)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    rocblas_handle h;
+    if (int rc = blas_for(op, as_stream(stream), &h))
+        return rc;
+    // y [M x Vp] = x [M x C] wte^T
+    return gemm_rm(op, h, false, true, (int)rows, vocab_size_padded, hidden_size, 1.f, x, hidden_size, wte,
+                   hidden_size, 0.f, y, vocab_size_padded);
+}
+
+int gpt_hip_unembedding_backward_f32(float *grad_x, float *grad_wte, const float *grad_y, const float *x,
+                                     const float *wte, int batch_size, int seq_len, int hidden_size,
+                                     int vocab_size_padded, void *stream)
+{
+    static const char *op = "gpt_hip_unembedding_backward_f32";
+    long rows = 0;
+    if (int rc = check_rows(op, batch_size, seq_len, (long long)hidden_size + vocab_size_padded, &rows))
+        return rc;
+    if (hidden_size <= 0 || vocab_size_padded <= 0)
+        return fail(GPT_HIP_OPS_EINVAL, "%s: hidden_size %d, vocab_size_padded %d", op, hidden_size,
+                    vocab_size_padded);
+    if (rows == 0)
+        return 0;
+    if (!grad_x || !grad_wte || !grad_y || !x || !wte)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    rocblas_handle h;
+    if (int rc = blas_for(op, as_stream(stream), &h))
+        return rc;
+    const int M = (int)rows, C = hidden_size, V = vocab_size_padded;
+    // grad_x [M x C] = grad_y [M x V] wte [V x C]
+    if (int rc = gemm_rm(op, h, false, false, M, C, V, 1.f, grad_y, V, wte, C, 0.f, grad_x, C))
+        return rc;
+    // grad_wte [V x C] += grad_y^T [V x M] x [M x C]
+    return gemm_rm(op, h, true, false, V, C, M, 1.f, grad_y, V, x, C, 1.f, grad_wte, C);
+}
+
+int gpt_hip_layernorm_residual_forward_f32(float *y, float *means, float *vars, float *x, const float *residual,
+                                           const float *gamma, const float *beta, int batch_size, int seq_len,
+                                           int hidden_size, void *stream)
+{
+    static const char *op = "gpt_hip_layernorm_residual_forward_f32";
+    long rows = 0;
+    if (int rc = check_rows(op, batch_size, seq_len, hidden_size, &rows))
+        return rc;
+    if (rows == 0)
+        return 0;
+    if (!y || !means || !vars || !x || !gamma || !beta)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    return launched(op, gpt_ops::launch_layernorm_fwd(y, means, vars, x, residual, gamma, beta, rows, hidden_size,
+                                                      as_stream(stream)));
+}
+
+int gpt_hip_layernorm_residual_backward_f32(float *grad_x, float *grad_gamma, float *grad_beta, const float *grad_y,
+                                            const float *grad_residual, const float *x, const float *means,
+                                            const float *vars, const float *gamma, int batch_size, int seq_len,
+                                            int hidden_size, void *stream)
+{
+    static const char *op = "gpt_hip_layernorm_residual_backward_f32";
+    long rows = 0;
+    if (int rc = check_rows(op, batch_size, seq_len, hidden_size, &rows))
+        return rc;
+    if (rows == 0)
+        return 0;
+    if (!grad_x || !grad_gamma || !grad_beta || !grad_y || !x || !means || !vars || !gamma)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    const hipStream_t st = as_stream(stream);
+    float *ws = nullptr;
+    if (int rc = ws_alloc(op, &ws, (size_t)gpt_ops::colsum_parts(rows) * 2 * hidden_size, st))
+        return rc;
+    const int rc = launched(op, gpt_ops::launch_layernorm_bwd(grad_x, grad_gamma, grad_beta, grad_y, grad_residual,
+                                                              x, means, vars, gamma, rows, hidden_size, ws, st));
+    const int rf = ws_free(op, ws, st);
+    return rc ? rc : rf;
+}
+
+int gpt_hip_linear_activation_forward_f32(float *y, float *act, const float *x, const float *w, const float *b,
+                                          int activation, int batch_size, int seq_len, int input_size,
+                                          int output_size, void *stream)
+{
+    static const char *op = "gpt_hip_linear_activation_forward_f32";
+    long rows = 0;
+    if (int rc = check_rows(op, batch_size, seq_len, (long long)input_size + output_size, &rows))
+        return rc;
+    if (input_size <= 0 || output_size <= 0)
+        return fail(GPT_HIP_OPS_EINVAL, "%s: input_size %d, output_size %d", op, input_size, output_size);
+    if (rows == 0)
+        return 0;
+    if (!y || !x || !w || !b || (activation && !act))
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    const hipStream_t st = as_stream(stream);
+    rocblas_handle h;
+    if (int rc = blas_for(op, st, &h))
+        return rc;
+    // y [M x N] = x [M x K] w [K x N], then + b (and GELU) in one pass
+    if (int rc = gemm_rm(op, h, false, false, (int)rows, output_size, input_size, 1.f, x, input_size, w,
+                         output_size, 0.f, y, output_size))
+        return rc;
+    return launched(op, gpt_ops::launch_bias_gelu(y, activation ? act : nullptr, b, rows, output_size, st));
+}
+
+int gpt_hip_linear_backward_f32(float *grad_x, float *grad_w, float *grad_b, const float *grad_y, const float *x,
+                                const float *w, int batch_size, int seq_len, int input_size, int output_size,
+                                void *stream)
+{
+    static const char *op = "gpt_hip_linear_backward_f32";
+    long rows = 0;
+    if (int rc = check_rows(op, batch_size, seq_len, (long long)input_size + output_size, &rows))
+        return rc;
+    if (input_size <= 0 || output_size <= 0)
+        return fail(GPT_HIP_OPS_EINVAL, "%s: input_size %d, output_size %d", op, input_size, output_size);
+    if (rows == 0)
+        return 0;
+    if (!grad_x || !grad_w || !grad_b || !grad_y || !x || !w)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    const hipStream_t st = as_stream(stream);
+    rocblas_handle h;
+    if (int rc = blas_for(op, st, &h))
+        return rc;
+    const int M = (int)rows, K = input_size, N = output_size;
+    // grad_x [M x K] = grad_y [M x N] w^T [N x K]
+    if (int rc = gemm_rm(op, h, false, true, M, K, N, 1.f, grad_y, N, w, N, 0.f, grad_x, K))
+        return rc;
+    // grad_w [K x N] += x^T [K x M] grad_y [M x N]
+    if (int rc = gemm_rm(op, h, true, false, K, N, M, 1.f, x, K, grad_y, N, 1.f, grad_w, N))
+        return rc;
+    float *ws = nullptr;
+    if (int rc = ws_alloc(op, &ws, (size_t)gpt_ops::colsum_parts(rows) * N, st))
+        return rc;
+    const int rc = launched(op, gpt_ops::launch_bias_grad(grad_b, grad_y, rows, N, ws, st));
+    const int rf = ws_free(op, ws, st);
+    return rc ? rc : rf;
+}
+
+int gpt_hip_activation_backward_f32(float *grad_x, const float *grad_y, const float *x, int batch_size,
+                                    int seq_len, int output_size, void *stream)
+{
+    static const char *op = "gpt_hip_activation_backward_f32";
+    long rows = 0;
+    if (int rc = check_rows(op, batch_size, seq_len, output_size, &rows))
+        return rc;
+    if (rows == 0)
+        return 0;
+    if (!grad_x || !grad_y || !x)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    return launched(op, gpt_ops::launch_gelu_bwd(grad_x, grad_y, x, rows * output_size, as_stream(stream)));
+}
+
+int gpt_hip_softmax_forward_f32(float *y, const float *x, int batch_size, int seq_len, int vocab_size,
+                                int vocab_size_padded, void *stream)
+{
+    static const char *op = "gpt_hip_softmax_forward_f32";
+    long rows = 0;
+    if (int rc = check_rows(op, batch_size, seq_len, vocab_size_padded, &rows))
+        return rc;
+    if (vocab_size <= 0 || vocab_size > vocab_size_padded)
+        return fail(GPT_HIP_OPS_EINVAL, "%s: vocab_size %d, vocab_size_padded %d", op, vocab_size,
+                    vocab_size_padded);
+    if (rows == 0)
+        return 0;
+    if (!y || !x)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    return launched(op, gpt_ops::launch_softmax_fwd(y, x, rows, vocab_size, vocab_size_padded, as_stream(stream)));
+}
+
+int gpt_hip_cross_entropy_softmax_backward_f32(float *grad_x, const float *y_softmax, const int *tokens_labels,
+                                               int batch_size, int seq_len, int vocab_size, int vocab_size_padded,
+                                               void *stream)
+{
+    static const char *op = "gpt_hip_cross_entropy_softmax_backward_f32";
+    long rows = 0;
+    if (int rc = check_rows(op, batch_size, seq_len, vocab_size_padded, &rows))
+        return rc;
+    if (vocab_size <= 0 || vocab_size > vocab_size_padded)
+        return fail(GPT_HIP_OPS_EINVAL, "%s: vocab_size %d, vocab_size_padded %d", op, vocab_size,
+                    vocab_size_padded);
+    if (rows == 0)
+        return 0;
+    if (!grad_x || !y_softmax || !tokens_labels)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    return launched(op, gpt_ops::launch_ce_bwd(grad_x, y_softmax, tokens_labels, rows, vocab_size,
+                                               vocab_size_padded, as_stream(stream)));
+}
+
+int gpt_hip_cross_entropy_loss_f32(float *loss, const float *y_softmax, const int *tokens_labels, int batch_size,
+                                   int seq_len, int vocab_size_padded, void *stream)
+{
+    static const char *op = "gpt_hip_cross_entropy_loss_f32";
+    long rows = 0;
+    if (int rc = check_rows(op, batch_size, seq_len, vocab_size_padded, &rows))
+        return rc;
+    if (!loss)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (rows == 0)
+        return 0;
+    if (!y_softmax || !tokens_labels)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    return launched(op, gpt_ops::launch_ce_loss(loss, y_softmax, tokens_labels, rows, vocab_size_padded,
+                                                as_stream(stream)));
+}
+
+int gpt_hip_adamw_step_f32(float *params, float *g, float *m, float *v, int size, float lr, float beta1,
+                           float beta2, float eps, float weight_decay, int step, void *stream)
+{
+    static const char *op = "gpt_hip_adamw_step_f32";
+    if (size < 0)
+        return fail(GPT_HIP_OPS_EINVAL, "%s: size %d", op, size);
+    if (size == 0)
+        return 0;
+    if (!params || !g || !m || !v)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    // bias corrections exactly as the CPU backend forms them (cpu_backend.cpp:519-520, 526-527)
+    const float one_m_b1p = 1.0f - powf(beta1, (float)step);
+    const float one_m_b2p = 1.0f - powf(beta2, (float)step);
+    return launched(op, gpt_ops::launch_adamw(params, g, m, v, size, lr, beta1, beta2, eps, weight_decay, one_m_b1p,
+                                              one_m_b2p, as_stream(stream)));
+}
+
+int gpt_hip_scale_and_clip_grad_f32(float *g, int size, float max_norm, int accum_steps, void *stream)
+{
+    static const char *op = "gpt_hip_scale_and_clip_grad_f32";
+    if (size < 0 || accum_steps < 1)
+        return fail(GPT_HIP_OPS_EINVAL, "%s: size %d, accum_steps %d", op, size, accum_steps);
+    if (size == 0)
+        return 0;
+    if (!g)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    const hipStream_t st = as_stream(stream);
+    float *ws = nullptr;
+    if (int rc = ws_alloc(op, &ws, (size_t)gpt_ops::clip_parts(), st))
+        return rc;
+    const int rc = launched(op, gpt_ops::launch_scale_clip(g, size, max_norm, (float)accum_steps, ws, st));
+    const int rf = ws_free(op, ws, st);
+    return rc ? rc : rf;
+}
+
+int gpt_hip_fill_normal_f32(float *ptr, float mean, float stddev, size_t size, unsigned long long seed,
+                            void *stream)
+{
+    static const char *op = "gpt_hip_fill_normal_f32";
+    if (size == 0)
+        return 0;
+    if (!ptr)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    return launched(op, gpt_ops::launch_fill_normal(ptr, size, mean, stddev, seed, as_stream(stream)));
+}
+
+int gpt_hip_fill_const_f32(float *ptr, float value, size_t size, void *stream)
+{
+    static const char *op = "gpt_hip_fill_const_f32";
+    if (size == 0)
+        return 0;
+    if (!ptr)
+        return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    return launched(op, gpt_ops::launch_fill_const(ptr, size, value, as_stream(stream)));
+}
+
+const char *gpt_hip_ops_last_error(void) { return g_err; }
+
+}  // extern "C"
