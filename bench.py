@@ -33,6 +33,10 @@ Usage:
                                                             for every prefix T=1..256 (the reference's
                                                             generation loop without a KV cache); one
                                                             JSON line of its own
+  python bench.py --ops [--no-cpu]                          the GPT-2 124M ops around attention
+                                                            (gpt_amd/libgpt_hip_ops.so) at the C3
+                                                            shapes, each against its roofline; one
+                                                            JSON line of its own
   python bench.py --copy-calibration                        256 MiB device copy x5
                                                             (run under --pmc)
   python bench.py --traffic KERNEL FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
@@ -127,6 +131,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--prefix-sweep", action="store_true",
                     help="time BASELINE config 5(b) (forward, B=1, T=1..256) instead of the headline")
+    ap.add_argument("--ops", action="store_true",
+                    help="time the GPT-2 ops around attention (libgpt_hip_ops.so) instead of the headline")
     ap.add_argument("--bwd-path", type=int, default=0, choices=(0, 2),
                     help="backward variant for profiling: 0 deterministic dS-tile dQ (default), "
                          "2 fp32-atomic dQ (gpt_hip_attn_set_path)")
@@ -242,6 +248,237 @@ def prefix_sweep(args):
     print(json.dumps(out), flush=True)
 
 
+# GPT-2 124M around the attention path at the C3 shapes (B=16, T=256): d_model
+# 768, d_ffn 3072, vocabulary 50257 padded to 50304, 12 layers, max_seq_len 256
+# (reference src/train/train.cpp:63-70; weights gpt.cpp:38-84; the call
+# sequence of GPT::forward / GPT::backward, gpt.cpp:431-641, and the
+# optimizer step, gpt.cpp:643-676).
+F_FFN, VOCAB, VOCAB_P = 3072, 50257, 50304
+PEAK_HBM_GBS = 8000.0
+
+
+def ops_bench(args):
+    """Each op of one GPT-2 124M training step other than attention, at the
+    step's shapes, through gpt_amd.ops (the C ABI of libgpt_hip_ops.so), with
+    resident device inputs: median of `reps` event-timed calls on the current
+    stream. HBM-bound ops are scored by algorithmic bytes (each operand read
+    or written once) against 8 TB/s, GEMM ops by 2 M N K FLOPs per product
+    against the fp32 MFMA peak. `per_step` is how many calls of that shape one
+    training step makes; `step_ms` = sum of per_step x time over these ops and
+    the attention op pair (12 layers, timed here too), i.e. a whole step's GPU
+    time when the calls run back to back."""
+    import numpy as np
+    import torch
+
+    import gpt_amd
+    from gpt_amd import ops
+
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream()
+    M, Cm = B * T, C
+    rng = np.random.default_rng(1240)
+    n_params = (VOCAB_P * Cm + T * Cm  # wte, wpe (max_seq_len 256, train.cpp:64)
+                + LAYERS * (2 * Cm + 3 * Cm * Cm + 3 * Cm + Cm * Cm + Cm + 2 * Cm + 2 * Cm * F_FFN + F_FFN + Cm)
+                + 2 * Cm)
+
+    def randn(*shape, scale=1.0):
+        return torch.randn(*shape, device=dev) * scale
+
+    tok = torch.from_numpy(rng.integers(0, VOCAB, size=M).astype(np.int32)).to(dev)
+    n_unique = int(np.unique(tok.cpu().numpy()).size)
+    f4 = 4
+    cases = []  # (name, per_step, bound, work, fn)
+
+    wte, wpe = randn(VOCAB_P, Cm, scale=0.02), randn(T, Cm, scale=0.02)
+    y = torch.empty(M, Cm, device=dev)
+    cases.append(("embedding_forward", 1, "hbm", f4 * (2 * M * Cm + T * Cm + M),
+                  lambda: ops.device_embedding_forward(y, wte, wpe, tok, B, T, Cm, VOCAB_P, st)))
+    gwte, gwpe, gy = torch.zeros(VOCAB_P, Cm, device=dev), torch.zeros(T, Cm, device=dev), randn(M, Cm)
+    cases.append(("embedding_backward", 1, "hbm", f4 * (M * Cm + M + 2 * n_unique * Cm + 2 * T * Cm),
+                  lambda: ops.device_embedding_backward(gwte, gwpe, gy, tok, B, T, Cm, VOCAB_P, st)))
+
+    x, res, lny = randn(M, Cm), randn(M, Cm), torch.empty(M, Cm, device=dev)
+    gam, bet = 1 + randn(Cm, scale=0.1), randn(Cm, scale=0.1)
+    mu, var = torch.empty(M, device=dev), torch.empty(M, device=dev)
+    cases.append(("layernorm_residual_forward", 2 * LAYERS + 1, "hbm", f4 * (4 * M * Cm + 2 * Cm + 2 * M),
+                  lambda: ops.device_layernorm_residual_fused_forward(lny, mu, var, x, res, gam, bet, B, T, Cm, st)))
+    lgx, gres, ggam, gbet = torch.empty(M, Cm, device=dev), randn(M, Cm), torch.zeros(Cm, device=dev), \
+        torch.zeros(Cm, device=dev)
+    cases.append(("layernorm_residual_backward", 2 * LAYERS + 1, "hbm", f4 * (4 * M * Cm + 2 * M + 5 * Cm),
+                  lambda: ops.device_layernorm_residual_fused_backward(lgx, ggam, gbet, gy, gres, x, mu, var, gam,
+                                                                       B, T, Cm, st)))
+
+    for tag, k_in, n_out, act in (("qkv", Cm, 3 * Cm, False), ("attn_proj", Cm, Cm, False),
+                                  ("ffn_up", Cm, F_FFN, True), ("ffn_down", F_FFN, Cm, False)):
+        xi, w, bb = randn(M, k_in), randn(k_in, n_out, scale=k_in ** -0.5), randn(n_out, scale=0.1)
+        yo, ao = torch.empty(M, n_out, device=dev), torch.empty(M, n_out, device=dev) if act else None
+        cases.append((f"linear_forward_{tag}", LAYERS, "mfma", 2 * M * k_in * n_out,
+                      lambda xi=xi, w=w, bb=bb, yo=yo, ao=ao, k_in=k_in, n_out=n_out, act=act:
+                      ops.device_linear_activation_fused_forward(yo, ao, xi, w, bb, act, B, T, k_in, n_out, st)))
+        gyo, gxi = randn(M, n_out), torch.empty(M, k_in, device=dev)
+        gw, gb = torch.zeros(k_in, n_out, device=dev), torch.zeros(n_out, device=dev)
+        cases.append((f"linear_backward_{tag}", LAYERS, "mfma", 4 * M * k_in * n_out,
+                      lambda gxi=gxi, gw=gw, gb=gb, gyo=gyo, xi=xi, w=w, k_in=k_in, n_out=n_out:
+                      ops.device_linear_backward(gxi, gw, gb, gyo, xi, w, B, T, k_in, n_out, st)))
+    ga, gyf, xf = torch.empty(M, F_FFN, device=dev), randn(M, F_FFN), randn(M, F_FFN)
+    cases.append(("activation_backward", LAYERS, "hbm", f4 * 3 * M * F_FFN,
+                  lambda: ops.device_activation_backward(ga, gyf, xf, B, T, F_FFN, st)))
+
+    logits, probs = torch.empty(M, VOCAB_P, device=dev), torch.empty(M, VOCAB_P, device=dev)
+    cases.append(("unembedding_forward", 1, "mfma", 2 * M * Cm * VOCAB_P,
+                  lambda: ops.device_unembedding_forward(logits, x, wte, B, T, Cm, VOCAB_P, st)))
+    cases.append(("softmax_forward", 1, "hbm", f4 * 2 * M * VOCAB_P,
+                  lambda: ops.device_softmax_forward(probs, logits, B, T, VOCAB, VOCAB_P, st)))
+    gl = torch.zeros(M, VOCAB_P, device=dev)
+    cases.append(("cross_entropy_softmax_backward", 1, "hbm", f4 * (2 * M * VOCAB + M),
+                  lambda: ops.device_cross_entropy_softmax_fused_backward(gl, probs, tok, B, T, VOCAB, VOCAB_P, st)))
+    loss = torch.empty(1, device=dev)
+    cases.append(("cross_entropy_loss", 1, "hbm", f4 * 2 * M,
+                  lambda: ops.device_cross_entropy_loss(loss, probs, tok, B, T, VOCAB_P, st)))
+    gxu = torch.empty(M, Cm, device=dev)
+    cases.append(("unembedding_backward", 1, "mfma", 4 * M * Cm * VOCAB_P,
+                  lambda: ops.device_unembedding_backward(gxu, gwte, gl, x, wte, B, T, Cm, VOCAB_P, st)))
+
+    prm, grd = randn(n_params, scale=0.02), randn(n_params, scale=1e-3)
+    m1, v1 = torch.zeros(n_params, device=dev), torch.zeros(n_params, device=dev)
+    cases.append(("adamw_step", 1, "hbm", f4 * 7 * n_params,
+                  lambda: ops.device_adamw_step(prm, grd, m1, v1, n_params, 6e-4, 0.9, 0.95, 1e-8, 0.1, 1, st)))
+    cases.append(("scale_and_clip_grad", 1, "hbm", f4 * 3 * n_params,
+                  lambda: ops.device_scale_and_clip_grad(grd, n_params, 1e9, 1, st)))
+
+    # the attention op pair of one layer, for the step total
+    qkv = randn(B, T, 3 * Cm)
+    ya, la = torch.empty(B, T, Cm, device=dev), torch.empty(B, T, H, device=dev)
+    gqkv, Dc, dya = torch.empty(B, T, 3 * Cm, device=dev), torch.empty(B, T, H, device=dev), randn(B, T, Cm)
+    cases.append(("attention_forward", LAYERS, "mfma", attn_flops(B, T, H, D_HEAD, bwd=False),
+                  lambda: gpt_amd.device_flash_attention_forward(ya, la, qkv, B, T, Cm, H, st)))
+    cases.append(("attention_backward", LAYERS, "mfma", attn_flops(B, T, H, D_HEAD, fwd=False),
+                  lambda: gpt_amd.device_flash_attention_backward(gqkv, Dc, la, dya, ya, qkv, B, T, Cm, H, st)))
+
+    reps = max(5, args.steps // 2)
+    res_ops = {}
+    step_ms = 0.0
+    for name, per_step, bound, work, fn in cases:
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        torch.cuda._sleep(5_000_000)  # queue the reps behind a GPU spin: time the GPU, not the launches
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for e0, e1 in ev:
+            e0.record(st)
+            fn()
+            e1.record(st)
+        torch.cuda.synchronize()
+        us = float(np.median([a.elapsed_time(b) for a, b in ev])) * 1e3
+        if bound == "hbm":
+            ach, peak, unit = work / (us * 1e-6) / 1e9, PEAK_HBM_GBS, "GB/s"
+        else:
+            ach, peak, unit = work / (us * 1e-6) / 1e12, PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
+        res_ops[name] = {"us": round(us, 2), "per_step": per_step, "bound": bound,
+                         ("bytes" if bound == "hbm" else "flops"): work, "achieved": round(ach, 2), "unit": unit,
+                         "frac": round(ach / peak, 4)}
+        step_ms += per_step * us / 1e3
+    out = {
+        "metric": "GPT-2 124M training-step ops on one MI355X: per-op GPU time vs roofline, B=16 T=256",
+        "n_gpus": 1,
+        "dtype": "fp32",
+        "data": "synthetic (torch.randn / uniform token ids)",
+        "config": {"workload": "every IGPTBackend compute op of one GPT-2 124M step at B=16 T=256 "
+                               "(12 layers, d_model 768, d_ffn 3072, vocab 50257 padded to 50304)",
+                   "params": n_params, "reps": reps},
+        "ops": res_ops,
+        "step_ms": round(step_ms, 3),
+        "peaks": {"hbm_GBs": PEAK_HBM_GBS, "fp32_mfma_TFLOPs": PEAK_FP32_MFMA_TFLOPS},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = ops_cpu_baseline(res_ops)
+    print(json.dumps(out), flush=True)
+
+
+def ops_cpu_baseline(res_ops):
+    """The reference CPUBackend ops (oracle/_ref, -O3, one thread) on bounded
+    samples of the same shapes (a few rows each, the rest of the shape as in
+    the step); each op's time is scaled to the step's rows, and `step_s` is
+    the whole step at that rate."""
+    import numpy as np
+
+    from oracle import pyoracle, pyops
+
+    impl, kind = ("ref_fast", "reference") if pyoracle.ref_available(fast=True) else ("oracle", "port")
+    rng = np.random.default_rng(7)
+    Cm = C
+
+    def rnd(*shape, s=1.0):
+        return (rng.standard_normal(shape) * s).astype(np.float32)
+
+    per_op = {}
+
+    def timed(name, rows, fn, scale_rows):
+        t0 = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t0
+        per_op[name] = {"sample_rows": rows, "s_at_step_shape": round(dt * scale_rows / rows, 4)}
+
+    Mfull = B * T
+    r = 64
+    tok = rng.integers(0, VOCAB, size=r).astype(np.int32)
+    wte, wpe = rnd(VOCAB_P, Cm, s=0.02), rnd(T, Cm, s=0.02)
+    timed("embedding_forward", r, lambda: pyops.embedding_forward(np.zeros((r, Cm), np.float32), wte, wpe, tok, 1, r,
+                                                                   Cm, impl), Mfull)
+    gw = np.zeros_like(wte)
+    timed("embedding_backward", r, lambda: pyops.embedding_backward(gw, np.zeros((T, Cm), np.float32),
+                                                                     rnd(r, Cm), tok, 1, r, Cm, impl), Mfull)
+    r = 512
+    x, res = rnd(r, Cm), rnd(r, Cm)
+    g_, b_ = rnd(Cm), rnd(Cm)
+    mu, var = np.zeros(r, np.float32), np.zeros(r, np.float32)
+    timed("layernorm_residual_forward", r, lambda: pyops.layernorm_forward(np.zeros((r, Cm), np.float32), mu, var, x,
+                                                                            res, g_, b_, 1, r, Cm, impl), Mfull)
+    timed("layernorm_residual_backward", r, lambda: pyops.layernorm_backward(
+        np.zeros((r, Cm), np.float32), np.zeros(Cm, np.float32), np.zeros(Cm, np.float32), rnd(r, Cm), rnd(r, Cm), x,
+        mu, var, g_, 1, r, Cm, impl), Mfull)
+    r = 8
+    for tag, k_in, n_out, act in (("qkv", Cm, 3 * Cm, False), ("attn_proj", Cm, Cm, False),
+                                  ("ffn_up", Cm, F_FFN, True), ("ffn_down", F_FFN, Cm, False)):
+        xi, w, bb = rnd(r, k_in), rnd(k_in, n_out, s=0.03), rnd(n_out)
+        timed(f"linear_forward_{tag}", r, lambda: pyops.linear_forward(
+            np.zeros((r, n_out), np.float32), np.zeros((r, n_out), np.float32), xi, w, bb, act, 1, r, k_in, n_out,
+            impl), Mfull)
+        timed(f"linear_backward_{tag}", r, lambda: pyops.linear_backward(
+            np.zeros((r, k_in), np.float32), np.zeros((k_in, n_out), np.float32), np.zeros(n_out, np.float32),
+            rnd(r, n_out), xi, w, 1, r, k_in, n_out, impl), Mfull)
+    r = 256
+    timed("activation_backward", r, lambda: pyops.activation_backward(np.zeros((r, F_FFN), np.float32), rnd(r, F_FFN),
+                                                                       rnd(r, F_FFN), 1, r, F_FFN, impl), Mfull)
+    r = 2
+    xu = rnd(r, Cm)
+    timed("unembedding_forward", r, lambda: pyops.unembedding_forward(np.zeros((r, VOCAB_P), np.float32), xu, wte, 1,
+                                                                       r, Cm, VOCAB_P, impl), Mfull)
+    timed("unembedding_backward", r, lambda: pyops.unembedding_backward(
+        np.zeros((r, Cm), np.float32), np.zeros_like(wte), rnd(r, VOCAB_P, s=1e-4), xu, wte, 1, r, Cm, VOCAB_P, impl),
+        Mfull)
+    r = 64
+    lg = rnd(r, VOCAB_P, s=3.0)
+    pr = np.zeros_like(lg)
+    labels = rng.integers(0, VOCAB, size=r).astype(np.int32)
+    timed("softmax_forward", r, lambda: pyops.softmax_forward(pr, lg, 1, r, VOCAB, VOCAB_P, impl), Mfull)
+    timed("cross_entropy_softmax_backward", r, lambda: pyops.ce_backward(np.zeros_like(lg), pr, labels, 1, r, VOCAB,
+                                                                          VOCAB_P, impl), Mfull)
+    timed("cross_entropy_loss", r, lambda: pyops.ce_loss(pr, labels, 1, r, VOCAB_P, impl), Mfull)
+    n = 1 << 22
+    p_, g2 = rnd(n, s=0.02), rnd(n, s=1e-3)
+    n_params = res_ops["adamw_step"]["bytes"] // 28
+    timed("adamw_step", n, lambda: pyops.adamw(p_, g2, np.zeros(n, np.float32), np.zeros(n, np.float32), n, 6e-4, 0.9,
+                                               0.95, 1e-8, 0.1, 1, impl), n_params)
+    timed("scale_and_clip_grad", n, lambda: pyops.scale_clip(g2, n, 1e9, 1, impl), n_params)
+    step_s = sum(res_ops[k]["per_step"] * v["s_at_step_shape"] for k, v in per_op.items())
+    gpu_ms = sum(v["per_step"] * v["us"] for k, v in res_ops.items() if k in per_op) / 1e3
+    return {"value": round(step_s, 3), "unit": "s per step (these ops, attention excluded)", "cores": 1,
+            "kind": kind, "gpu_ms_same_ops": round(gpu_ms, 3),
+            "sample": "each op on a few rows of its step shape (sample_rows), time scaled to the step's rows",
+            "ops": per_op}
+
+
 def main():
     args = parse()
     if args.traffic:
@@ -256,6 +493,9 @@ def main():
         sys.exit(2)
     if args.prefix_sweep:
         prefix_sweep(args)
+        return
+    if args.ops:
+        ops_bench(args)
         return
 
     import numpy as np
