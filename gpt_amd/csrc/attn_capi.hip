@@ -10,7 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
-#include <atomic>
+#include <mutex>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -20,8 +20,6 @@ namespace {
 thread_local char g_err[512] = "";
 int g_path = 0;  // 0 automatic, 1 general-d kernels only, 2 atomic-dQ backward
 
-constexpr int kMaxDevices = 64;
-std::atomic<int> g_pool_ready[kMaxDevices];
 
 int fail(int code, const char *fmt, ...)
 {
@@ -83,30 +81,65 @@ struct LaunchTimer
 };
 LaunchTimer g_timer;
 
-// Stream-ordered dS workspace for the deterministic backward. The device's
-// default memory pool is told to keep freed memory (release threshold = max),
-// so after the first call hipMallocAsync / hipFreeAsync hand the same block
-// back without a device allocation; concurrent calls on different streams
-// each get their own block.
-hipError_t workspace_alloc(void **p, size_t bytes, hipStream_t st)
+// dS workspace of the deterministic backward: one grow-only buffer per
+// (device, stream), allocated on first use and kept until the process ends.
+// Calls on one stream run in order and share its buffer; calls on different
+// streams get different buffers. (A stream-ordered hipMallocAsync /
+// hipFreeAsync pair per call measured about 13 us of GPU time per call on
+// MI355X, even with the pool keeping its memory.)
+struct Workspace
+{
+    int dev;
+    hipStream_t st;
+    void *p;
+    size_t bytes;
+};
+constexpr int kMaxWorkspaces = 64;
+std::mutex g_ws_mu;
+Workspace g_ws[kMaxWorkspaces];
+int g_ws_n = 0;
+
+hipError_t workspace_get(void **out, size_t bytes, hipStream_t st)
 {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess)
         return e;
-    if (dev >= 0 && dev < kMaxDevices && g_pool_ready[dev].load(std::memory_order_acquire) == 0)
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    Workspace *w = nullptr;
+    for (int i = 0; i < g_ws_n; ++i)
+        if (g_ws[i].dev == dev && g_ws[i].st == st)
+            w = &g_ws[i];
+    if (!w)
     {
-        hipMemPool_t pool;
-        e = hipDeviceGetDefaultMemPool(&pool, dev);
-        if (e != hipSuccess)
-            return e;
-        uint64_t keep = UINT64_MAX;
-        e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
-        if (e != hipSuccess)
-            return e;
-        g_pool_ready[dev].store(1, std::memory_order_release);
+        if (g_ws_n == kMaxWorkspaces)
+            return hipErrorOutOfMemory;
+        w = &g_ws[g_ws_n++];
+        *w = Workspace{dev, st, nullptr, 0};
     }
-    return hipMallocAsync(p, bytes, st);
+    if (w->bytes < bytes)
+    {
+        if (w->p)
+        {
+            // the old buffer may still be read by work queued on this stream
+            e = hipStreamSynchronize(st);
+            if (e == hipSuccess)
+                e = hipFree(w->p);
+            if (e != hipSuccess)
+                return e;
+            w->p = nullptr;
+            w->bytes = 0;
+        }
+        e = hipMalloc(&w->p, bytes);
+        if (e != hipSuccess)
+        {
+            w->p = nullptr;
+            return e;
+        }
+        w->bytes = bytes;
+    }
+    *out = w->p;
+    return hipSuccess;
 }
 
 }  // namespace
@@ -192,15 +225,12 @@ int gpt_hip_attn_bwd_f32(float *grad_x, float *D_cache, const float *lse, const 
     int chunk = 0;
     const size_t bytes = gpt_attn::bwd_d64_workspace_bytes(s, &chunk);
     void *ws = nullptr;
-    hipError_t e = workspace_alloc(&ws, bytes, st);
+    hipError_t e = workspace_get(&ws, bytes, st);
     if (e != hipSuccess)
         return fail(GPT_HIP_ATTN_ENOMEM, "%s: workspace of %zu bytes: %s", op, bytes, hipGetErrorString(e));
     e = gpt_attn::launch_bwd_d64(grad_x, D_cache, lse, grad_y, y, qkv, static_cast<float *>(ws), chunk, s, st);
-    const hipError_t ef = hipFreeAsync(ws, st);
     if (e != hipSuccess)
         return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
-    if (ef != hipSuccess)
-        return fail(GPT_HIP_ATTN_ELAUNCH, "%s: workspace release failed: %s", op, hipGetErrorString(ef));
     return 0;
 }
 

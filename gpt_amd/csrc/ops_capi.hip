@@ -1,7 +1,7 @@
 // C ABI of the gfx950 GPT-2 ops around the attention path (declared in
 // include/gpt_hip_ops.h): argument validation, rocBLAS GEMMs for the matrix
 // products, launches of the element-wise / normalisation / reduction kernels
-// (ops_kernels.hip), status codes.
+// (ops_kernels.hip), the reductions' workspace, status codes.
 //
 // The reference's op methods return void and abort on any runtime error
 // (src/backend/cuda/utils/cuda_utils.cuh:21-34); here every entry point returns
@@ -108,42 +108,60 @@ int gemm_rm(const char *op, rocblas_handle h, bool ta, bool tb, int M, int N, in
 
 // ---------------------------------------------------------------- workspace
 
-std::mutex g_pool_mu;
-bool g_pool_ready[kMaxDevices] = {};
+// Partial-sum workspace (at most a few MB: 256 partial rows), one grow-only
+// buffer per (device, stream), kept until the process ends. Calls on one
+// stream run in order, so they can share its buffer; calls on different
+// streams get different buffers. (A stream-ordered hipMallocAsync /
+// hipFreeAsync pair per call measured ~10 us of GPU time per call here,
+// more than the reductions it serves.)
+struct Workspace
+{
+    int dev;
+    hipStream_t st;
+    float *p;
+    size_t floats;
+};
+constexpr int kMaxWorkspaces = 64;
+std::mutex g_ws_mu;
+Workspace g_ws[kMaxWorkspaces];
+int g_ws_n = 0;
 
-// Stream-ordered workspace from the device's default memory pool, told once
-// per device to keep freed memory, so steady-state calls do not allocate.
-int ws_alloc(const char *op, float **p, size_t floats, hipStream_t st)
+int ws_get(const char *op, float **out, size_t floats, hipStream_t st)
 {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    if (hipGetDevice(&dev) != hipSuccess)
         return fail(GPT_HIP_OPS_ENODEV, "%s: no current HIP device", op);
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    Workspace *w = nullptr;
+    for (int i = 0; i < g_ws_n; ++i)
+        if (g_ws[i].dev == dev && g_ws[i].st == st)
+            w = &g_ws[i];
+    if (!w)
     {
-        std::lock_guard<std::mutex> lock(g_pool_mu);
-        if (!g_pool_ready[dev])
-        {
-            hipMemPool_t pool;
-            uint64_t keep = UINT64_MAX;
-            if (hipDeviceGetDefaultMemPool(&pool, dev) != hipSuccess ||
-                hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep) != hipSuccess)
-                return fail(GPT_HIP_OPS_ENOMEM, "%s: default memory pool unavailable", op);
-            g_pool_ready[dev] = true;
-        }
+        if (g_ws_n == kMaxWorkspaces)
+            return fail(GPT_HIP_OPS_ENOMEM, "%s: more than %d (device, stream) workspaces", op, kMaxWorkspaces);
+        w = &g_ws[g_ws_n++];
+        *w = Workspace{dev, st, nullptr, 0};
     }
-    void *q = nullptr;
-    const hipError_t e = hipMallocAsync(&q, floats * sizeof(float), st);
-    if (e != hipSuccess)
-        return fail(GPT_HIP_OPS_ENOMEM, "%s: workspace of %zu bytes: %s", op, floats * sizeof(float),
-                    hipGetErrorString(e));
-    *p = static_cast<float *>(q);
-    return 0;
-}
-
-int ws_free(const char *op, float *p, hipStream_t st)
-{
-    const hipError_t e = hipFreeAsync(p, st);
-    if (e != hipSuccess)
-        return fail(GPT_HIP_OPS_ELAUNCH, "%s: workspace release failed: %s", op, hipGetErrorString(e));
+    if (w->floats < floats)
+    {
+        if (w->p)
+        {
+            // the old buffer may still be read by work queued on this stream
+            if (hipStreamSynchronize(st) != hipSuccess || hipFree(w->p) != hipSuccess)
+                return fail(GPT_HIP_OPS_ELAUNCH, "%s: workspace release failed", op);
+            w->p = nullptr;
+            w->floats = 0;
+        }
+        void *q = nullptr;
+        const hipError_t e = hipMalloc(&q, floats * sizeof(float));
+        if (e != hipSuccess)
+            return fail(GPT_HIP_OPS_ENOMEM, "%s: workspace of %zu bytes: %s", op, floats * sizeof(float),
+                        hipGetErrorString(e));
+        w->p = static_cast<float *>(q);
+        w->floats = floats;
+    }
+    *out = w->p;
     return 0;
 }
 
@@ -274,12 +292,10 @@ int gpt_hip_layernorm_residual_backward_f32(float *grad_x, float *grad_gamma, fl
         return rc;
     const hipStream_t st = as_stream(stream);
     float *ws = nullptr;
-    if (int rc = ws_alloc(op, &ws, (size_t)gpt_ops::colsum_parts(rows) * 2 * hidden_size, st))
+    if (int rc = ws_get(op, &ws, (size_t)gpt_ops::colsum_parts(rows) * 2 * hidden_size, st))
         return rc;
-    const int rc = launched(op, gpt_ops::launch_layernorm_bwd(grad_x, grad_gamma, grad_beta, grad_y, grad_residual,
-                                                              x, means, vars, gamma, rows, hidden_size, ws, st));
-    const int rf = ws_free(op, ws, st);
-    return rc ? rc : rf;
+    return launched(op, gpt_ops::launch_layernorm_bwd(grad_x, grad_gamma, grad_beta, grad_y, grad_residual, x, means,
+                                                      vars, gamma, rows, hidden_size, ws, st));
 }
 
 int gpt_hip_linear_activation_forward_f32(float *y, float *act, const float *x, const float *w, const float *b,
@@ -337,11 +353,9 @@ int gpt_hip_linear_backward_f32(float *grad_x, float *grad_w, float *grad_b, con
     if (int rc = gemm_rm(op, h, true, false, K, N, M, 1.f, x, K, grad_y, N, 1.f, grad_w, N))
         return rc;
     float *ws = nullptr;
-    if (int rc = ws_alloc(op, &ws, (size_t)gpt_ops::colsum_parts(rows) * N, st))
+    if (int rc = ws_get(op, &ws, (size_t)gpt_ops::colsum_parts(rows) * N, st))
         return rc;
-    const int rc = launched(op, gpt_ops::launch_bias_grad(grad_b, grad_y, rows, N, ws, st));
-    const int rf = ws_free(op, ws, st);
-    return rc ? rc : rf;
+    return launched(op, gpt_ops::launch_bias_grad(grad_b, grad_y, rows, N, ws, st));
 }
 
 int gpt_hip_activation_backward_f32(float *grad_x, const float *grad_y, const float *x, int batch_size,
@@ -451,11 +465,9 @@ int gpt_hip_scale_and_clip_grad_f32(float *g, int size, float max_norm, int accu
         return rc;
     const hipStream_t st = as_stream(stream);
     float *ws = nullptr;
-    if (int rc = ws_alloc(op, &ws, (size_t)gpt_ops::clip_parts(), st))
+    if (int rc = ws_get(op, &ws, (size_t)gpt_ops::clip_parts(), st))
         return rc;
-    const int rc = launched(op, gpt_ops::launch_scale_clip(g, size, max_norm, (float)accum_steps, ws, st));
-    const int rf = ws_free(op, ws, st);
-    return rc ? rc : rf;
+    return launched(op, gpt_ops::launch_scale_clip(g, size, max_norm, (float)accum_steps, ws, st));
 }
 
 int gpt_hip_fill_normal_f32(float *ptr, float mean, float stddev, size_t size, unsigned long long seed,

@@ -385,24 +385,27 @@ __global__ __launch_bounds__(256) void layernorm_fwd_generic_kernel(float *__res
         y[r * C + h] = (xr[h] - mean) / den * gamma[h] + beta[h];
 }
 
-// LayerNorm backward for the rows of one stripe (4 waves x rpw rows, one
+// LayerNorm backward for the rows of one stripe (NW waves x rpw rows, one
 // wave per row, the row in registers), CPU backend cpu_backend.cpp:177-211:
 //   x_hat = (x - mean) * inv_std, a = grad_y * gamma,
 //   grad_x = inv_std * (a - sum(a) / C - x_hat * sum(a * x_hat) / C)
 //            (+ grad_residual).
-// Each lane also sums grad_y * x_hat and grad_y over its rows for its
-// columns; the 4 waves' sums are added in wave order through LDS and stored
-// as the stripe's partial row part[stripe] = [gamma sums | beta sums].
-template <int NV>
-__global__ __launch_bounds__(256) void layernorm_bwd_kernel(float *__restrict__ gx, const float *__restrict__ gy,
-                                                            const float *__restrict__ gres,
-                                                            const float *__restrict__ x,
-                                                            const float *__restrict__ means,
-                                                            const float *__restrict__ vars,
-                                                            const float *__restrict__ gamma,
-                                                            float *__restrict__ part, long rows, int C, int rpw)
+// A wave takes its rows two at a time, issuing both rows' loads before the
+// first row's sums. Each lane also sums grad_y * x_hat and grad_y over its
+// rows for its columns; the NW waves' sums are added in wave order through
+// LDS and stored as the stripe's partial row part[stripe] = [gamma sums |
+// beta sums].
+template <int NV, int NW>
+__global__ __launch_bounds__(NW * 64) void layernorm_bwd_kernel(float *__restrict__ gx,
+                                                                const float *__restrict__ gy,
+                                                                const float *__restrict__ gres,
+                                                                const float *__restrict__ x,
+                                                                const float *__restrict__ means,
+                                                                const float *__restrict__ vars,
+                                                                const float *__restrict__ gamma,
+                                                                float *__restrict__ part, long rows, int C, int rpw)
 {
-    extern __shared__ float4 lds4[];  // [4][2][C / 4]
+    extern __shared__ float4 lds4[];  // [NW][2][C / 4]
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, C4 = C >> 2;
     const float4 *gm4 = reinterpret_cast<const float4 *>(gamma);
     float4 gm[NV], pg[NV], pb[NV];
@@ -413,30 +416,33 @@ __global__ __launch_bounds__(256) void layernorm_bwd_kernel(float *__restrict__ 
         gm[k] = i < C4 ? gm4[i] : f4(0.f);
         pg[k] = pb[k] = f4(0.f);
     }
-    const long r0 = ((long)blockIdx.x * 4 + w) * rpw;
-    for (int j = 0; j < rpw; ++j)
-    {
-        const long r = r0 + j;
-        if (r >= rows)
-            break;
-        const float mean = means[r];
-        const float inv_std = 1.0f / sqrtf(vars[r] + kLnEps);
-        const float4 *gy4 = reinterpret_cast<const float4 *>(gy + r * C);
-        const float4 *x4 = reinterpret_cast<const float4 *>(x + r * C);
-        float4 g[NV], xh[NV];
-        float s1 = 0.f, s2 = 0.f;
+    auto load = [&](long r, float4(&g)[NV], float4(&xv)[NV], float4(&e)[NV]) {
 #pragma unroll
         for (int k = 0; k < NV; ++k)
         {
             const int i = lane + 64 * k;
-            g[k] = xh[k] = f4(0.f);
+            g[k] = xv[k] = e[k] = f4(0.f);
             if (i < C4)
             {
-                g[k] = gy4[i];
-                const float4 xv = x4[i];
-                xh[k] = make_float4((xv.x - mean) * inv_std, (xv.y - mean) * inv_std, (xv.z - mean) * inv_std,
-                                    (xv.w - mean) * inv_std);
+                g[k] = reinterpret_cast<const float4 *>(gy + r * C)[i];
+                xv[k] = reinterpret_cast<const float4 *>(x + r * C)[i];
+                if (gres)
+                    e[k] = reinterpret_cast<const float4 *>(gres + r * C)[i];
             }
+        }
+    };
+    auto row = [&](long r, float mean, float var, const float4(&g)[NV], const float4(&xv)[NV],
+                   const float4(&e)[NV]) {
+        const float inv_std = 1.0f / sqrtf(var + kLnEps);
+        float4 xh[NV];
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+        {
+            xh[k] = make_float4((xv[k].x - mean) * inv_std, (xv[k].y - mean) * inv_std, (xv[k].z - mean) * inv_std,
+                                (xv[k].w - mean) * inv_std);
+            if (lane + 64 * k >= C4)
+                xh[k] = f4(0.f);
             const float ax = g[k].x * gm[k].x, ay = g[k].y * gm[k].y, az = g[k].z * gm[k].z, aw = g[k].w * gm[k].w;
             s1 += (ax + ay) + (az + aw);
             s2 += (ax * xh[k].x + ay * xh[k].y) + (az * xh[k].z + aw * xh[k].w);
@@ -445,7 +451,6 @@ __global__ __launch_bounds__(256) void layernorm_bwd_kernel(float *__restrict__ 
         }
         const float m1 = wave_sum(s1) / (float)C, m2 = wave_sum(s2) / (float)C;
         float4 *gx4 = reinterpret_cast<float4 *>(gx + r * C);
-        const float4 *gr4 = reinterpret_cast<const float4 *>(gres + r * C);
 #pragma unroll
         for (int k = 0; k < NV; ++k)
         {
@@ -457,10 +462,31 @@ __global__ __launch_bounds__(256) void layernorm_bwd_kernel(float *__restrict__ 
                                        inv_std * (g[k].z * gm[k].z - m1 - xh[k].z * m2),
                                        inv_std * (g[k].w * gm[k].w - m1 - xh[k].w * m2));
                 if (gres)
-                    o = add4(o, gr4[i]);
+                    o = add4(o, e[k]);
                 gx4[i] = o;
             }
         }
+    };
+    const long r0 = ((long)blockIdx.x * NW + w) * rpw;
+    for (int j = 0; j < rpw; j += 2)
+    {
+        const long ra = r0 + j, rb = ra + 1;
+        if (ra >= rows)
+            break;
+        const bool has_b = j + 1 < rpw && rb < rows;
+        float4 ga[NV], xa[NV], ea[NV], gb[NV], xb[NV], eb[NV];
+        load(ra, ga, xa, ea);
+        const float mean_a = means[ra], var_a = vars[ra];
+        float mean_b = 0.f, var_b = 0.f;
+        if (has_b)
+        {
+            load(rb, gb, xb, eb);
+            mean_b = means[rb];
+            var_b = vars[rb];
+        }
+        row(ra, mean_a, var_a, ga, xa, ea);
+        if (has_b)
+            row(rb, mean_b, var_b, gb, xb, eb);
     }
 #pragma unroll
     for (int k = 0; k < NV; ++k)
@@ -474,11 +500,11 @@ __global__ __launch_bounds__(256) void layernorm_bwd_kernel(float *__restrict__ 
     }
     __syncthreads();
     float4 *p4 = reinterpret_cast<float4 *>(part + (long)blockIdx.x * 2 * C);
-    for (int i = threadIdx.x; i < 2 * C4; i += 256)
+    for (int i = threadIdx.x; i < 2 * C4; i += NW * 64)
     {
         const int which = i / C4, c = i % C4;
         float4 t = lds4[(0 * 2 + which) * C4 + c];
-        for (int ww = 1; ww < 4; ++ww)
+        for (int ww = 1; ww < NW; ++ww)
             t = add4(t, lds4[(ww * 2 + which) * C4 + c]);
         p4[i] = t;
     }
@@ -529,17 +555,26 @@ __global__ __launch_bounds__(256) void layernorm_bwd_generic_kernel(
 
 // out0[c] += sum_p part[p][c] (c < N0), out1[c - N0] += ... (N0 <= c < N):
 // one workgroup of 16 waves per 64 columns; wave k adds partial rows
-// p = k, k + 16, ... in order, then the 16 wave sums are added in wave order.
+// p = k, k + 16, ... (at most 16 of them: parts <= 256) in order, all loads
+// issued first, then the 16 wave sums are added in wave order.
 __global__ __launch_bounds__(1024) void colsum_final_kernel(float *__restrict__ out0, float *__restrict__ out1,
                                                             const float *__restrict__ part, int parts, int N, int N0)
 {
     __shared__ float red[16][64];
     const int lane = threadIdx.x & 63, k = threadIdx.x >> 6;
     const int c = blockIdx.x * 64 + lane;
-    float s = 0.f;
-    if (c < N)
-        for (int p = k; p < parts; p += 16)
-            s += part[(long)p * N + c];
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+    {
+        const int p = k + 16 * j;
+        v[j] = (c < N && p < parts) ? part[(long)p * N + c] : 0.f;
+    }
+    float s = v[0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j)
+        if (k + 16 * j < parts)
+            s += v[j];
     red[k][lane] = s;
     __syncthreads();
     if (k == 0 && c < N)
@@ -810,20 +845,42 @@ __global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ p, const
     const long stride = (long)gridDim.x * 256;
     if (V4)
     {
+        // two float4 of each stream per iteration, all eight loads issued first
         float4 *p4 = reinterpret_cast<float4 *>(p), *m4 = reinterpret_cast<float4 *>(m),
                *v4 = reinterpret_cast<float4 *>(v);
         const float4 *g4 = reinterpret_cast<const float4 *>(g);
-        for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < (n >> 2); i += stride)
+        const long n4 = n >> 2;
+        for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += 2 * stride)
         {
-            float4 pp = p4[i], mm = m4[i], vv = v4[i];
-            const float4 gg = g4[i];
-            adamw_one(pp.x, gg.x, mm.x, vv.x, lr, beta1, beta2, eps, wd, one_m_b1p, one_m_b2p);
-            adamw_one(pp.y, gg.y, mm.y, vv.y, lr, beta1, beta2, eps, wd, one_m_b1p, one_m_b2p);
-            adamw_one(pp.z, gg.z, mm.z, vv.z, lr, beta1, beta2, eps, wd, one_m_b1p, one_m_b2p);
-            adamw_one(pp.w, gg.w, mm.w, vv.w, lr, beta1, beta2, eps, wd, one_m_b1p, one_m_b2p);
-            p4[i] = pp;
-            m4[i] = mm;
-            v4[i] = vv;
+            const long i2 = i + stride;
+            const bool two = i2 < n4;
+            float4 pa = p4[i], ma = m4[i], va = v4[i];
+            const float4 ga = g4[i];
+            float4 pb = f4(0.f), mb = f4(0.f), vb = f4(0.f), gb = f4(0.f);
+            if (two)
+            {
+                pb = p4[i2];
+                mb = m4[i2];
+                vb = v4[i2];
+                gb = g4[i2];
+            }
+            adamw_one(pa.x, ga.x, ma.x, va.x, lr, beta1, beta2, eps, wd, one_m_b1p, one_m_b2p);
+            adamw_one(pa.y, ga.y, ma.y, va.y, lr, beta1, beta2, eps, wd, one_m_b1p, one_m_b2p);
+            adamw_one(pa.z, ga.z, ma.z, va.z, lr, beta1, beta2, eps, wd, one_m_b1p, one_m_b2p);
+            adamw_one(pa.w, ga.w, ma.w, va.w, lr, beta1, beta2, eps, wd, one_m_b1p, one_m_b2p);
+            p4[i] = pa;
+            m4[i] = ma;
+            v4[i] = va;
+            if (two)
+            {
+                adamw_one(pb.x, gb.x, mb.x, vb.x, lr, beta1, beta2, eps, wd, one_m_b1p, one_m_b2p);
+                adamw_one(pb.y, gb.y, mb.y, vb.y, lr, beta1, beta2, eps, wd, one_m_b1p, one_m_b2p);
+                adamw_one(pb.z, gb.z, mb.z, vb.z, lr, beta1, beta2, eps, wd, one_m_b1p, one_m_b2p);
+                adamw_one(pb.w, gb.w, mb.w, vb.w, lr, beta1, beta2, eps, wd, one_m_b1p, one_m_b2p);
+                p4[i2] = pb;
+                m4[i2] = mb;
+                v4[i2] = vb;
+            }
         }
     }
     else
@@ -839,7 +896,7 @@ __global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ p, const
     }
 }
 
-constexpr int kClipParts = 1024;
+constexpr int kClipParts = 4096;
 
 // Partial sums of (g / accum)^2 over fixed stripes: workgroup p covers
 // elements [p * stripe, (p + 1) * stripe) (stripe a multiple of 4); g is not
@@ -951,11 +1008,12 @@ __global__ __launch_bounds__(256) void fill_const_kernel(float *__restrict__ p, 
 }
 
 // Stripe of rows per partial for the column reductions: at most 256
-// partials, at least 16 rows per stripe, a multiple of 4 (one share per wave).
+// partials, at least 16 rows per stripe, a multiple of 8 (equal shares for
+// the 8 or 4 waves of a LayerNorm-backward workgroup).
 long colsum_rows_per_part(long rows)
 {
     long rps = (rows + 255) / 256;
-    rps = (rps + 3) & ~3L;
+    rps = (rps + 7) & ~7L;
     return rps < 16 ? 16 : rps;
 }
 
@@ -1038,27 +1096,37 @@ hipError_t launch_layernorm_bwd(float *gx, float *ggamma, float *gbeta, const fl
     const int parts = colsum_parts(rows);
     const bool v4 = C % 4 == 0 && C <= 2048 && al16(gx) && al16(gy) && al16(x) && al16(gamma) &&
                     (!gres || al16(gres));
-    const dim3 grid((unsigned)parts), blk(256);
-    const int rpw = (int)(rps / 4);
-    const size_t lds = (size_t)8 * C * sizeof(float);
+    const dim3 grid((unsigned)parts);
     if (!v4)
-        hipLaunchKernelGGL(layernorm_bwd_generic_kernel, grid, blk, 0, st, gx, gy, gres, x, means, vars, gamma, ws,
-                           rows, C, (int)rps);
-    else if (C <= 256)
-        hipLaunchKernelGGL(layernorm_bwd_kernel<1>, grid, blk, lds, st, gx, gy, gres, x, means, vars, gamma, ws,
-                           rows, C, rpw);
-    else if (C <= 512)
-        hipLaunchKernelGGL(layernorm_bwd_kernel<2>, grid, blk, lds, st, gx, gy, gres, x, means, vars, gamma, ws,
-                           rows, C, rpw);
-    else if (C <= 768)
-        hipLaunchKernelGGL(layernorm_bwd_kernel<3>, grid, blk, lds, st, gx, gy, gres, x, means, vars, gamma, ws,
-                           rows, C, rpw);
+    {
+        hipLaunchKernelGGL(layernorm_bwd_generic_kernel, grid, dim3(256), 0, st, gx, gy, gres, x, means, vars, gamma,
+                           ws, rows, C, (int)rps);
+    }
     else if (C <= 1024)
-        hipLaunchKernelGGL(layernorm_bwd_kernel<4>, grid, blk, lds, st, gx, gy, gres, x, means, vars, gamma, ws,
-                           rows, C, rpw);
+    {
+        // 8 waves per stripe (rps is a multiple of 8): 2 rows a wave at B*T = 4096
+        const int rpw = (int)(rps / 8);
+        const size_t lds = (size_t)16 * C * sizeof(float);
+        const dim3 blk(512);
+        if (C <= 256)
+            hipLaunchKernelGGL((layernorm_bwd_kernel<1, 8>), grid, blk, lds, st, gx, gy, gres, x, means, vars, gamma,
+                               ws, rows, C, rpw);
+        else if (C <= 512)
+            hipLaunchKernelGGL((layernorm_bwd_kernel<2, 8>), grid, blk, lds, st, gx, gy, gres, x, means, vars, gamma,
+                               ws, rows, C, rpw);
+        else if (C <= 768)
+            hipLaunchKernelGGL((layernorm_bwd_kernel<3, 8>), grid, blk, lds, st, gx, gy, gres, x, means, vars, gamma,
+                               ws, rows, C, rpw);
+        else
+            hipLaunchKernelGGL((layernorm_bwd_kernel<4, 8>), grid, blk, lds, st, gx, gy, gres, x, means, vars, gamma,
+                               ws, rows, C, rpw);
+    }
     else
-        hipLaunchKernelGGL(layernorm_bwd_kernel<8>, grid, blk, lds, st, gx, gy, gres, x, means, vars, gamma, ws,
-                           rows, C, rpw);
+    {
+        const int rpw = (int)(rps / 4);
+        hipLaunchKernelGGL((layernorm_bwd_kernel<8, 4>), grid, dim3(256), (size_t)8 * C * sizeof(float), st, gx, gy,
+                           gres, x, means, vars, gamma, ws, rows, C, rpw);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;

@@ -19,11 +19,12 @@
  *   - Softmax scale is 1/sqrt(d); the causal mask keeps key j <= query i.
  *   - `stream` is a hipStream_t passed as void*; NULL means the default stream.
  *     Work is enqueued asynchronously. The forward allocates nothing. The
- *     head_dim-64 backward takes a stream-ordered dS workspace from the
- *     device's default memory pool (hipMallocAsync / hipFreeAsync on
- *     `stream`; 4 KiB per 32x32 causal tile, 28 MiB at B=16 T=256 H=12, at
- *     most 2 GiB per call: larger problems run in (b, h) chunks); the pool is
- *     set to keep freed memory, so steady-state calls do not allocate.
+ *     head_dim-64 backward uses a dS workspace (4 KiB per 32x32 causal tile,
+ *     28 MiB at B=16 T=256 H=12, at most 2 GiB per call: larger problems run
+ *     in (b, h) chunks) that the library allocates on first use, one buffer
+ *     per (device, stream), grows when a call needs more (after waiting for
+ *     that stream) and keeps until the process ends; steady-state calls do
+ *     not allocate.
  *   - Return 0 on success or a negative GPT_HIP_ATTN_E* code; the message of
  *     the last failure on the calling thread is kept for
  *     gpt_hip_attn_last_error(). Inputs are never modified.

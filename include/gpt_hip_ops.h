@@ -26,8 +26,9 @@
  *     accumulate; the reference's CUDA backend uses TF32 tensor cores); the
  *     element-wise, normalisation and reduction work runs on this library's
  *     own HIP kernels. Reductions that need partial sums (LayerNorm and bias
- *     gradients, the gradient norm) take a stream-ordered workspace from the
- *     device's default memory pool, like the attention backward.
+ *     gradients, the gradient norm) use a workspace the library allocates on
+ *     first use, one per (device, stream), grown when a call needs more (at
+ *     most 256 partial rows: a few MB) and kept until the process ends.
  *   - Token ids must lie in [0, vocab_rows) where the entry point takes
  *     vocab_rows > 0; the reference's methods do not receive the vocabulary
  *     size and do not check, and vocab_rows = 0 keeps that behaviour.
