@@ -10,6 +10,7 @@
 #include "ops_internal.h"
 
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
 
 #include <math.h>
@@ -21,6 +22,8 @@
 namespace {
 
 thread_local char g_err[512] = "";
+// GELU in hipBLASLt's epilogue (1) or as this library's pass over y (0).
+bool g_fused_gelu = true;
 
 int fail(int code, const char *fmt, ...)
 {
@@ -118,6 +121,7 @@ struct Workspace
 {
     int dev;
     hipStream_t st;
+    int slot;  // 0 reduction partials, 1 GEMM workspace
     float *p;
     size_t floats;
 };
@@ -126,7 +130,7 @@ std::mutex g_ws_mu;
 Workspace g_ws[kMaxWorkspaces];
 int g_ws_n = 0;
 
-int ws_get(const char *op, float **out, size_t floats, hipStream_t st)
+int ws_get(const char *op, float **out, size_t floats, hipStream_t st, int slot = 0)
 {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess)
@@ -134,14 +138,14 @@ int ws_get(const char *op, float **out, size_t floats, hipStream_t st)
     std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace *w = nullptr;
     for (int i = 0; i < g_ws_n; ++i)
-        if (g_ws[i].dev == dev && g_ws[i].st == st)
+        if (g_ws[i].dev == dev && g_ws[i].st == st && g_ws[i].slot == slot)
             w = &g_ws[i];
     if (!w)
     {
         if (g_ws_n == kMaxWorkspaces)
             return fail(GPT_HIP_OPS_ENOMEM, "%s: more than %d (device, stream) workspaces", op, kMaxWorkspaces);
         w = &g_ws[g_ws_n++];
-        *w = Workspace{dev, st, nullptr, 0};
+        *w = Workspace{dev, st, slot, nullptr, 0};
     }
     if (w->floats < floats)
     {
@@ -163,6 +167,149 @@ int ws_get(const char *op, float **out, size_t floats, hipStream_t st)
     }
     *out = w->p;
     return 0;
+}
+
+// ---------------------------------------------------------------- hipBLASLt
+
+// Which library takes a GEMM is a fixed rule (use_lt), from measurements of
+// both on MI355X at the GPT-2 124M step shapes (random fp32 data, M = B T =
+// 4096): hipBLASLt's fp32 kernels win where the row-major product has at
+// most 1024 columns (x W with W 768 x 768: 49 vs 60 us; 3072 x 768: 159 vs
+// 186 us; grad_y wte: 2.05 vs 2.73 ms) and for the weight gradients x^T
+// grad_y (768 x 3072 over 4096 rows: 139 vs 237 us); rocBLAS wins on the
+// wide products (768 -> 2304 / 3072 columns, the 50304-column logits:
+// 2.15 vs 2.28 ms). hipBLASLt also fuses the linear layer's bias (and GELU)
+// into its epilogue. Either library's algorithm is fixed per shape, so
+// results are bitwise reproducible. One hipBLASLt plan (descriptor, layouts,
+// heuristic algorithm) per (device, shape, transposes, epilogue), built on
+// first use and kept; rocBLAS takes any shape hipBLASLt has no plan for.
+struct LtPlan
+{
+    int dev;
+    bool ta, tb;
+    int M, N, K, lda, ldb, ldc;
+    int epi;  // 0 none, 1 + bias, 2 + bias with GELU (pre-activation to aux)
+    bool ok;
+    hipblasLtMatmulDesc_t desc;
+    hipblasLtMatrixLayout_t la, lb, lc;
+    hipblasLtMatmulAlgo_t algo;
+    size_t ws;
+};
+constexpr int kMaxPlans = 256;
+constexpr size_t kLtMaxWorkspace = size_t(32) << 20;
+std::mutex g_lt_mu;
+hipblasLtHandle_t g_lt[kMaxDevices] = {};
+LtPlan g_plans[kMaxPlans];
+int g_nplans = 0;
+
+// Plan for row-major C[M x N] = op(A) op(B) (+ bias, GELU) on the current
+// device, or nullptr when hipBLASLt has none (the caller falls back to
+// rocBLAS). Called with g_lt_mu held.
+LtPlan *lt_plan(int dev, bool ta, bool tb, int M, int N, int K, int lda, int ldb, int ldc, int epi)
+{
+    for (int i = 0; i < g_nplans; ++i)
+    {
+        LtPlan &q = g_plans[i];
+        if (q.dev == dev && q.ta == ta && q.tb == tb && q.M == M && q.N == N && q.K == K && q.lda == lda &&
+            q.ldb == ldb && q.ldc == ldc && q.epi == epi)
+            return q.ok ? &q : nullptr;
+    }
+    if (g_nplans == kMaxPlans || dev < 0 || dev >= kMaxDevices)
+        return nullptr;
+    if (!g_lt[dev] && hipblasLtCreate(&g_lt[dev]) != HIPBLAS_STATUS_SUCCESS)
+    {
+        g_lt[dev] = nullptr;
+        return nullptr;
+    }
+    LtPlan &q = g_plans[g_nplans++];
+    q = LtPlan{dev, ta, tb, M, N, K, lda, ldb, ldc, epi, false, nullptr, nullptr, nullptr, nullptr, {}, 0};
+    // column-major view: C^T [N x M] = op(B)^T [N x K] op(A)^T [K x M]
+    const hipblasOperation_t opa = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+    const uint32_t ep = epi == 0 ? HIPBLASLT_EPILOGUE_DEFAULT
+                                 : epi == 1 ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_GELU_AUX_BIAS;
+    const int32_t f32 = HIP_R_32F;
+    const int64_t ld_aux = ldc;
+    if (hipblasLtMatmulDescCreate(&q.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatmulDescSetAttribute(q.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(opa)) ||
+        hipblasLtMatmulDescSetAttribute(q.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(opb)) ||
+        hipblasLtMatmulDescSetAttribute(q.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof(ep)))
+        return nullptr;
+    if (epi >= 1 && hipblasLtMatmulDescSetAttribute(q.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &f32, sizeof(f32)))
+        return nullptr;
+    if (epi == 2 &&
+        (hipblasLtMatmulDescSetAttribute(q.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE_AUX_LD, &ld_aux, sizeof(ld_aux)) ||
+         hipblasLtMatmulDescSetAttribute(q.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE_AUX_DATA_TYPE, &f32, sizeof(f32))))
+        return nullptr;
+    if (hipblasLtMatrixLayoutCreate(&q.la, HIP_R_32F, tb ? K : N, tb ? N : K, ldb) ||
+        hipblasLtMatrixLayoutCreate(&q.lb, HIP_R_32F, ta ? M : K, ta ? K : M, lda) ||
+        hipblasLtMatrixLayoutCreate(&q.lc, HIP_R_32F, N, M, ldc))
+        return nullptr;
+    hipblasLtMatmulPreference_t pref;
+    if (hipblasLtMatmulPreferenceCreate(&pref))
+        return nullptr;
+    size_t wmax = kLtMaxWorkspace;
+    hipblasLtMatmulHeuristicResult_t res[1];
+    int n = 0;
+    const bool found =
+        !hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wmax, sizeof(wmax)) &&
+        !hipblasLtMatmulAlgoGetHeuristic(g_lt[dev], q.desc, q.la, q.lb, q.lc, q.lc, pref, 1, res, &n) && n > 0 &&
+        res[0].state == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulPreferenceDestroy(pref);
+    if (!found)
+        return nullptr;
+    q.algo = res[0].algo;
+    q.ws = res[0].workspaceSize;
+    q.ok = true;
+    return &q;
+}
+
+// Row-major C[M x N] = alpha op(A) op(B) + beta C, with the epilogue: epi 1
+// adds bias[n] to every row; epi 2 also writes GELU of that to D and the
+// biased product to aux. Returns 1 when hipBLASLt has no plan (nothing was
+// enqueued), 0 on success, a GPT_HIP_OPS_E* code on failure.
+int lt_gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int K, float alpha, const float *A,
+            int lda, const float *B, int ldb, float beta, float *C, int ldc, int epi, const float *bias, float *aux)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess)
+        return fail(GPT_HIP_OPS_ENODEV, "%s: no current HIP device", op);
+    std::lock_guard<std::mutex> lock(g_lt_mu);
+    LtPlan *q = lt_plan(dev, ta, tb, M, N, K, lda, ldb, ldc, epi);
+    if (!q)
+        return 1;
+    float *ws = nullptr;
+    if (q->ws > 0)
+        if (int rc = ws_get(op, &ws, (q->ws + 3) / 4, st, 1))
+            return rc;
+    if (epi >= 1 &&
+        hipblasLtMatmulDescSetAttribute(q->desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)))
+        return fail(GPT_HIP_OPS_ELAUNCH, "%s: hipBLASLt bias attribute", op);
+    if (epi == 2 &&
+        hipblasLtMatmulDescSetAttribute(q->desc, HIPBLASLT_MATMUL_DESC_EPILOGUE_AUX_POINTER, &aux, sizeof(aux)))
+        return fail(GPT_HIP_OPS_ELAUNCH, "%s: hipBLASLt aux attribute", op);
+    const hipblasStatus_t s = hipblasLtMatmul(g_lt[dev], q->desc, &alpha, B, q->la, A, q->lb, &beta, C, q->lc, C,
+                                              q->lc, &q->algo, ws, q->ws, st);
+    if (s != HIPBLAS_STATUS_SUCCESS)
+        return fail(GPT_HIP_OPS_ELAUNCH, "%s: hipblasLtMatmul failed (%d)", op, (int)s);
+    return 0;
+}
+
+bool use_lt(bool ta, int N) { return ta || N <= 1024; }
+
+// Plain GEMM: hipBLASLt where use_lt says so and it has a plan, else rocBLAS.
+int gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int K, float alpha, const float *A, int lda,
+         const float *B, int ldb, float beta, float *C, int ldc)
+{
+    if (use_lt(ta, N))
+    {
+        const int rc = lt_gemm(op, st, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, 0, nullptr, nullptr);
+        if (rc != 1)
+            return rc;
+    }
+    rocblas_handle h;
+    if (int r = blas_for(op, st, &h))
+        return r;
+    return gemm_rm(op, h, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
 }
 
 hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
@@ -221,12 +368,9 @@ int gpt_hip_unembedding_forward_f32(float *y, const float *x, const float *wte, 
         return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
     if (int rc = check_device(op))
         return rc;
-    rocblas_handle h;
-    if (int rc = blas_for(op, as_stream(stream), &h))
-        return rc;
     // y [M x Vp] = x [M x C] wte^T
-    return gemm_rm(op, h, false, true, (int)rows, vocab_size_padded, hidden_size, 1.f, x, hidden_size, wte,
-                   hidden_size, 0.f, y, vocab_size_padded);
+    return gemm(op, as_stream(stream), false, true, (int)rows, vocab_size_padded, hidden_size, 1.f, x, hidden_size,
+                wte, hidden_size, 0.f, y, vocab_size_padded);
 }
 
 int gpt_hip_unembedding_backward_f32(float *grad_x, float *grad_wte, const float *grad_y, const float *x,
@@ -246,15 +390,13 @@ int gpt_hip_unembedding_backward_f32(float *grad_x, float *grad_wte, const float
         return fail(GPT_HIP_OPS_ENULL, "%s: NULL pointer", op);
     if (int rc = check_device(op))
         return rc;
-    rocblas_handle h;
-    if (int rc = blas_for(op, as_stream(stream), &h))
-        return rc;
+    const hipStream_t st = as_stream(stream);
     const int M = (int)rows, C = hidden_size, V = vocab_size_padded;
     // grad_x [M x C] = grad_y [M x V] wte [V x C]
-    if (int rc = gemm_rm(op, h, false, false, M, C, V, 1.f, grad_y, V, wte, C, 0.f, grad_x, C))
+    if (int rc = gemm(op, st, false, false, M, C, V, 1.f, grad_y, V, wte, C, 0.f, grad_x, C))
         return rc;
     // grad_wte [V x C] += grad_y^T [V x M] x [M x C]
-    return gemm_rm(op, h, true, false, V, C, M, 1.f, grad_y, V, x, C, 1.f, grad_wte, C);
+    return gemm(op, st, true, false, V, C, M, 1.f, grad_y, V, x, C, 1.f, grad_wte, C);
 }
 
 int gpt_hip_layernorm_residual_forward_f32(float *y, float *means, float *vars, float *x, const float *residual,
@@ -315,14 +457,37 @@ int gpt_hip_linear_activation_forward_f32(float *y, float *act, const float *x, 
     if (int rc = check_device(op))
         return rc;
     const hipStream_t st = as_stream(stream);
+    const int M = (int)rows, K = input_size, N = output_size;
+    // y [M x N] = x [M x K] w [K x N] + b. On hipBLASLt (use_lt) the bias goes
+    // in its epilogue, and with activation the GELU too when g_fused_gelu
+    // allows it (D = act, pre-activation y as the auxiliary output), else one
+    // pass of this library's GELU over y. On rocBLAS one pass adds the bias
+    // and writes the GELU.
+    if (!use_lt(false, N))
+    {
+        // rocBLAS below
+    }
+    else if (activation && g_fused_gelu)
+    {
+        const int rc = lt_gemm(op, st, false, false, M, N, K, 1.f, x, K, w, N, 0.f, act, N, 2, b, y);
+        if (rc != 1)
+            return rc;
+    }
+    else
+    {
+        const int rc = lt_gemm(op, st, false, false, M, N, K, 1.f, x, K, w, N, 0.f, y, N, 1, b, nullptr);
+        if (rc == 0)
+            return activation ? launched(op, gpt_ops::launch_gelu(act, y, rows, N, st)) : 0;
+        if (rc != 1)
+            return rc;
+    }
+    // no hipBLASLt plan: rocBLAS GEMM, then + b (and GELU) in one pass
     rocblas_handle h;
     if (int rc = blas_for(op, st, &h))
         return rc;
-    // y [M x N] = x [M x K] w [K x N], then + b (and GELU) in one pass
-    if (int rc = gemm_rm(op, h, false, false, (int)rows, output_size, input_size, 1.f, x, input_size, w,
-                         output_size, 0.f, y, output_size))
+    if (int rc = gemm_rm(op, h, false, false, M, N, K, 1.f, x, K, w, N, 0.f, y, N))
         return rc;
-    return launched(op, gpt_ops::launch_bias_gelu(y, activation ? act : nullptr, b, rows, output_size, st));
+    return launched(op, gpt_ops::launch_bias_gelu(y, activation ? act : nullptr, b, rows, N, st));
 }
 
 int gpt_hip_linear_backward_f32(float *grad_x, float *grad_w, float *grad_b, const float *grad_y, const float *x,
@@ -342,15 +507,12 @@ int gpt_hip_linear_backward_f32(float *grad_x, float *grad_w, float *grad_b, con
     if (int rc = check_device(op))
         return rc;
     const hipStream_t st = as_stream(stream);
-    rocblas_handle h;
-    if (int rc = blas_for(op, st, &h))
-        return rc;
     const int M = (int)rows, K = input_size, N = output_size;
     // grad_x [M x K] = grad_y [M x N] w^T [N x K]
-    if (int rc = gemm_rm(op, h, false, true, M, K, N, 1.f, grad_y, N, w, N, 0.f, grad_x, K))
+    if (int rc = gemm(op, st, false, true, M, K, N, 1.f, grad_y, N, w, N, 0.f, grad_x, K))
         return rc;
     // grad_w [K x N] += x^T [K x M] grad_y [M x N]
-    if (int rc = gemm_rm(op, h, true, false, K, N, M, 1.f, x, K, grad_y, N, 1.f, grad_w, N))
+    if (int rc = gemm(op, st, true, false, K, N, M, 1.f, x, K, grad_y, N, 1.f, grad_w, N))
         return rc;
     float *ws = nullptr;
     if (int rc = ws_get(op, &ws, (size_t)gpt_ops::colsum_parts(rows) * N, st))

@@ -27,6 +27,8 @@ hipError_t launch_layernorm_bwd(float *gx, float *ggamma, float *gbeta, const fl
 
 // y[r, o] += b[o]; act = GELU(y) when act != NULL
 hipError_t launch_bias_gelu(float *y, float *act, const float *b, long rows, int N, hipStream_t st);
+// act = GELU(y)
+hipError_t launch_gelu(float *act, const float *y, long rows, int N, hipStream_t st);
 // gb[o] += sum_r gy[r, o]; ws: colsum_parts(rows) * N floats
 hipError_t launch_bias_grad(float *gb, const float *gy, long rows, int N, float *ws, hipStream_t st);
 hipError_t launch_gelu_bwd(float *gx, const float *gy, const float *x, long n, hipStream_t st);

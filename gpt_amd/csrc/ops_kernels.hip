@@ -658,6 +658,26 @@ __global__ __launch_bounds__(256) void bias_gelu_kernel(float *__restrict__ y, f
     }
 }
 
+// act = GELU(y) (cpu_backend.cpp:234), grid-stride.
+template <bool V4>
+__global__ __launch_bounds__(256) void gelu_fwd_kernel(float *__restrict__ act, const float *__restrict__ y, long n)
+{
+    const long stride = (long)gridDim.x * 256;
+    if (V4)
+    {
+        for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < (n >> 2); i += stride)
+        {
+            const float4 s = reinterpret_cast<const float4 *>(y)[i];
+            reinterpret_cast<float4 *>(act)[i] = make_float4(gelu(s.x), gelu(s.y), gelu(s.z), gelu(s.w));
+        }
+    }
+    else
+    {
+        for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+            act[i] = gelu(y[i]);
+    }
+}
+
 // grad_x = grad_y * GELU'(x) (cpu_backend.cpp:268-287), grid-stride.
 template <bool V4>
 __global__ __launch_bounds__(256) void gelu_bwd_kernel(float *__restrict__ gx, const float *__restrict__ gy,
@@ -1143,6 +1163,16 @@ hipError_t launch_bias_gelu(float *y, float *act, const float *b, long rows, int
         hipLaunchKernelGGL(bias_gelu_kernel<true>, dim3(grid_for(n / 4, 256)), dim3(256), 0, st, y, act, b, n, N);
     else
         hipLaunchKernelGGL(bias_gelu_kernel<false>, dim3(grid_for(n, 256)), dim3(256), 0, st, y, act, b, n, N);
+    return hipGetLastError();
+}
+
+hipError_t launch_gelu(float *act, const float *y, long rows, int N, hipStream_t st)
+{
+    const long n = rows * N;
+    if (n % 4 == 0 && al16(act) && al16(y))
+        hipLaunchKernelGGL(gelu_fwd_kernel<true>, dim3(grid_for(n / 4, 256)), dim3(256), 0, st, act, y, n);
+    else
+        hipLaunchKernelGGL(gelu_fwd_kernel<false>, dim3(grid_for(n, 256)), dim3(256), 0, st, act, y, n);
     return hipGetLastError();
 }
 

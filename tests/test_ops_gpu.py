@@ -189,6 +189,31 @@ def test_linear_fwd_bwd(dev, B, T, n_in, n_out, activation):
     assert_close("GELU backward", host(ga), ga_r, RTOL)
 
 
+def test_gemm_ops_are_bitwise_repeatable(dev):
+    """The GEMM ops (hipBLASLt / rocBLAS algorithms chosen once per shape)
+    give the same bits on every call, accumulating outputs included."""
+    import torch
+
+    B, T, K, N, Vp = 4, 64, 768, 3072, 4096
+    r = rng(99)
+    x, w, b = to_dev(dev, f32(r.standard_normal((B, T, K)))), to_dev(dev, f32(r.standard_normal((K, N)) * 0.03)), \
+        to_dev(dev, f32(r.standard_normal(N)))
+    gy, wte = to_dev(dev, f32(r.standard_normal((B, T, N)))), to_dev(dev, f32(r.standard_normal((Vp, K)) * 0.02))
+    outs = []
+    for _ in range(2):
+        y, act = torch.empty((B, T, N), device=dev), torch.empty((B, T, N), device=dev)
+        ops.device_linear_activation_fused_forward(y, act, x, w, b, True, B, T, K, N)
+        gx, gw, gb = torch.empty((B, T, K), device=dev), torch.ones((K, N), device=dev), torch.ones(N, device=dev)
+        ops.device_linear_backward(gx, gw, gb, gy, x, w, B, T, K, N)
+        lg = torch.empty((B, T, Vp), device=dev)
+        ops.device_unembedding_forward(lg, x, wte, B, T, K, Vp)
+        ux, uw = torch.empty((B, T, K), device=dev), torch.ones((Vp, K), device=dev)
+        ops.device_unembedding_backward(ux, uw, lg, x, wte, B, T, K, Vp)
+        outs.append([host(t) for t in (y, act, gx, gw, gb, lg, ux, uw)])
+    for a, c in zip(*outs):
+        assert same_bits(a, c)
+
+
 @pytest.mark.parametrize("B,T,V,Vp", [(2, 8, 50257, 50304), (1, 5, 1000, 1003), (2, 3, 70000, 70000),
                                        (1, 4, 17, 20)])
 def test_softmax_cross_entropy(dev, B, T, V, Vp):
