@@ -9,8 +9,20 @@
 
 #include "hip_backend.h"
 
+#include <cstddef>
+
 class CUDABackend : public HipBackend
 {
 public:
     explicit CUDABackend(unsigned long seed = 42) : HipBackend(seed) {}
+
+    // The reference trainer deletes its backend before the GPT object and
+    // the data loader that still call it from their destructors
+    // (src/train/train.cpp:165-167 `delete backend; return 0;`, with `gpt`,
+    // line 76, and `loader`, line 92, still alive on the stack). The backend holds no resources of its
+    // own, so its storage is simply not released: those last device_free
+    // calls then reach a backend whose (empty) destructor has run but whose
+    // memory is intact, instead of freed memory.
+    static void operator delete(void *) noexcept {}
+    static void operator delete(void *, std::size_t) noexcept {}
 };

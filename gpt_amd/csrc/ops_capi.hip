@@ -121,7 +121,7 @@ struct Workspace
 {
     int dev;
     hipStream_t st;
-    int slot;  // 0 reduction partials, 1 GEMM workspace
+    int slot;  // one buffer per purpose (0: reduction partials)
     float *p;
     size_t floats;
 };
@@ -193,10 +193,9 @@ struct LtPlan
     hipblasLtMatmulDesc_t desc;
     hipblasLtMatrixLayout_t la, lb, lc;
     hipblasLtMatmulAlgo_t algo;
-    size_t ws;
+    size_t ws;  // always 0: only workspace-free algorithms are planned
 };
 constexpr int kMaxPlans = 256;
-constexpr size_t kLtMaxWorkspace = size_t(32) << 20;
 std::mutex g_lt_mu;
 hipblasLtHandle_t g_lt[kMaxDevices] = {};
 LtPlan g_plans[kMaxPlans];
@@ -247,20 +246,30 @@ LtPlan *lt_plan(int dev, bool ta, bool tb, int M, int N, int K, int lda, int ldb
     hipblasLtMatmulPreference_t pref;
     if (hipblasLtMatmulPreferenceCreate(&pref))
         return nullptr;
-    size_t wmax = kLtMaxWorkspace;
-    hipblasLtMatmulHeuristicResult_t res[1];
+    // Only algorithms that need no workspace: the split-K / stream-K kinds
+    // that do were seen to fail at launch with an internal error on some
+    // shapes, and their cross-workgroup reductions need not be reproducible.
+    size_t wmax = 0;
+    constexpr int kAsk = 8;
+    hipblasLtMatmulHeuristicResult_t res[kAsk];
     int n = 0;
-    const bool found =
+    const bool asked =
         !hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wmax, sizeof(wmax)) &&
-        !hipblasLtMatmulAlgoGetHeuristic(g_lt[dev], q.desc, q.la, q.lb, q.lc, q.lc, pref, 1, res, &n) && n > 0 &&
-        res[0].state == HIPBLAS_STATUS_SUCCESS;
+        !hipblasLtMatmulAlgoGetHeuristic(g_lt[dev], q.desc, q.la, q.lb, q.lc, q.lc, pref, kAsk, res, &n);
     hipblasLtMatmulPreferenceDestroy(pref);
-    if (!found)
+    if (!asked)
         return nullptr;
-    q.algo = res[0].algo;
-    q.ws = res[0].workspaceSize;
-    q.ok = true;
-    return &q;
+    for (int i = 0; i < n; ++i)
+    {
+        if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize == 0)
+        {
+            q.algo = res[i].algo;
+            q.ws = 0;
+            q.ok = true;
+            return &q;
+        }
+    }
+    return nullptr;
 }
 
 // Row-major C[M x N] = alpha op(A) op(B) + beta C, with the epilogue: epi 1
@@ -277,10 +286,6 @@ int lt_gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int 
     LtPlan *q = lt_plan(dev, ta, tb, M, N, K, lda, ldb, ldc, epi);
     if (!q)
         return 1;
-    float *ws = nullptr;
-    if (q->ws > 0)
-        if (int rc = ws_get(op, &ws, (q->ws + 3) / 4, st, 1))
-            return rc;
     if (epi >= 1 &&
         hipblasLtMatmulDescSetAttribute(q->desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)))
         return fail(GPT_HIP_OPS_ELAUNCH, "%s: hipBLASLt bias attribute", op);
@@ -288,13 +293,50 @@ int lt_gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int 
         hipblasLtMatmulDescSetAttribute(q->desc, HIPBLASLT_MATMUL_DESC_EPILOGUE_AUX_POINTER, &aux, sizeof(aux)))
         return fail(GPT_HIP_OPS_ELAUNCH, "%s: hipBLASLt aux attribute", op);
     const hipblasStatus_t s = hipblasLtMatmul(g_lt[dev], q->desc, &alpha, B, q->la, A, q->lb, &beta, C, q->lc, C,
-                                              q->lc, &q->algo, ws, q->ws, st);
+                                              q->lc, &q->algo, nullptr, 0, st);
     if (s != HIPBLAS_STATUS_SUCCESS)
-        return fail(GPT_HIP_OPS_ELAUNCH, "%s: hipblasLtMatmul failed (%d)", op, (int)s);
+    {
+        // refused before launching anything: this shape goes to rocBLAS from now on
+        q->ok = false;
+        return 1;
+    }
     return 0;
 }
 
 bool use_lt(bool ta, int N) { return ta || N <= 1024; }
+
+// Release the hipBLASLt plans and handles and the rocBLAS handles when the
+// library is unloaded (process exit included). This library is loaded after
+// hipBLASLt, rocBLAS and the HIP runtime, so it is finalised before them;
+// leaving the handles to those libraries' own teardown ended processes with a
+// segmentation fault after main() had returned.
+__attribute__((destructor)) void release_blas_handles()
+{
+    std::lock_guard<std::mutex> lock(g_lt_mu);
+    for (int i = 0; i < g_nplans; ++i)
+    {
+        LtPlan &q = g_plans[i];
+        if (q.la)
+            hipblasLtMatrixLayoutDestroy(q.la);
+        if (q.lb)
+            hipblasLtMatrixLayoutDestroy(q.lb);
+        if (q.lc)
+            hipblasLtMatrixLayoutDestroy(q.lc);
+        if (q.desc)
+            hipblasLtMatmulDescDestroy(q.desc);
+        q = LtPlan{};
+    }
+    g_nplans = 0;
+    for (int d = 0; d < kMaxDevices; ++d)
+    {
+        if (g_lt[d])
+            hipblasLtDestroy(g_lt[d]);
+        g_lt[d] = nullptr;
+        if (g_blas[d])
+            rocblas_destroy_handle(g_blas[d]);
+        g_blas[d] = nullptr;
+    }
+}
 
 // Plain GEMM: hipBLASLt where use_lt says so and it has a plan, else rocBLAS.
 int gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int K, float alpha, const float *A, int lda,
