@@ -16,10 +16,12 @@ class CUDABackend : public HipBackend
 public:
     explicit CUDABackend(unsigned long seed = 42) : HipBackend(seed) {}
 
-    // The reference trainer deletes its backend before the GPT object and
-    // the data loader that still call it from their destructors
-    // (src/train/train.cpp:165-167 `delete backend; return 0;`, with `gpt`,
-    // line 76, and `loader`, line 92, still alive on the stack). The backend holds no resources of its
+    // The reference trainer and generator delete their backend before the
+    // GPT object and the data loader / manager that still call it from their
+    // destructors (src/train/train.cpp:165-167 `delete backend; return 0;`,
+    // with `gpt`, line 76, and `loader`, line 92, still alive on the stack;
+    // src/infer/infer.cpp:166-169 with `gpt`, line 81, and `data_manager`,
+    // line 91). The backend holds no resources of its
     // own, so its storage is simply not released: those last device_free
     // calls then reach a backend whose (empty) destructor has run but whose
     // memory is intact, instead of freed memory.
