@@ -305,39 +305,6 @@ int lt_gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int 
 
 bool use_lt(bool ta, int N) { return ta || N <= 1024; }
 
-// Release the hipBLASLt plans and handles and the rocBLAS handles when the
-// library is unloaded (process exit included). This library is loaded after
-// hipBLASLt, rocBLAS and the HIP runtime, so it is finalised before them;
-// leaving the handles to those libraries' own teardown ended processes with a
-// segmentation fault after main() had returned.
-__attribute__((destructor)) void release_blas_handles()
-{
-    std::lock_guard<std::mutex> lock(g_lt_mu);
-    for (int i = 0; i < g_nplans; ++i)
-    {
-        LtPlan &q = g_plans[i];
-        if (q.la)
-            hipblasLtMatrixLayoutDestroy(q.la);
-        if (q.lb)
-            hipblasLtMatrixLayoutDestroy(q.lb);
-        if (q.lc)
-            hipblasLtMatrixLayoutDestroy(q.lc);
-        if (q.desc)
-            hipblasLtMatmulDescDestroy(q.desc);
-        q = LtPlan{};
-    }
-    g_nplans = 0;
-    for (int d = 0; d < kMaxDevices; ++d)
-    {
-        if (g_lt[d])
-            hipblasLtDestroy(g_lt[d]);
-        g_lt[d] = nullptr;
-        if (g_blas[d])
-            rocblas_destroy_handle(g_blas[d]);
-        g_blas[d] = nullptr;
-    }
-}
-
 // Plain GEMM: hipBLASLt where use_lt says so and it has a plan, else rocBLAS.
 int gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int K, float alpha, const float *A, int lda,
          const float *B, int ldb, float beta, float *C, int ldc)
