@@ -897,20 +897,28 @@ hipError_t launch_fwd_d64(float *y, float *lse, const float *qkv, const Shape &s
         nw = 1;
     timer_begin(kKindFwd, st);
     const int n_qg = (s.T + 63) / 64;
-    if ((long)n_qg * BH >= 256)
+    const int n_g = (s.T + 15) / 16;
+    const long groups = (long)n_qg * BH;
+    // Long rows over few (b, h): below 512 64-query groups the Q-stationary
+    // kernel's heaviest group (2 T / 32 key blocks on one workgroup) sets its
+    // time, and the split-key kernel, 8 waves per 16-query group, is faster
+    // (B=1 T=2048: 78.6 vs 98.7 us; B=2 T=1024: 50.4 vs 55.6 us; at 768
+    // groups and more it is not: B=1 T=4096 257 vs 224 us, B=4 T=1024 90.9 vs
+    // 69.3 us).
+    const bool long_rows = groups >= 256 && groups < 512 && s.T >= 1024;
+    if (groups >= 256 && !long_rows)
     {
         // enough 64-query groups to fill the GPU: the Q-stationary kernel
-        hipLaunchKernelGGL(fwd_qs_d64_kernel, dim3((unsigned)((long)n_qg * BH)), dim3(256), 0, st, y, lse, qkv, s.T,
-                           s.C, s.H, BH, n_qg, c2, fwd_cu_count());
+        hipLaunchKernelGGL(fwd_qs_d64_kernel, dim3((unsigned)groups), dim3(256), 0, st, y, lse, qkv, s.T, s.C, s.H,
+                           BH, n_qg, c2, fwd_cu_count());
         timer_end(st);
         return hipGetLastError();
     }
-    const int n_g = (s.T + 15) / 16;
-    if ((long)n_g * BH <= 512)
+    if (long_rows || (long)n_g * BH <= 512)
     {
-        // very small call (at most 2 workgroups per CU): the split-key kernel,
-        // one workgroup per 16-query group, up to 8 waves splitting its key
-        // blocks (one block each up to T = 256). Measured faster than the pair
+        // very small call (at most 2 workgroups per CU), or long rows over few
+        // (b, h): the split-key kernel, one workgroup per 16-query group, up
+        // to 8 waves splitting its key blocks (one block each up to T = 256). Measured faster than the pair
         // kernel up to this size (B=1 T=256: 9.6 vs 15.0 us; B=1 T=512: 15.5
         // vs 19.8 us; B=2 T=256: 11.7 vs 15.4 us), slower past it (B=2 T=512:
         // 22.3 vs 20.8 us; B=1 T=1024: 31.6 vs 30.3 us).

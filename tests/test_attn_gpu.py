@@ -116,12 +116,13 @@ def test_growing_scores_fwd_bwd(dev, T):
     check_fwd_bwd(dev, x, g, H, tag=f"growing T={T}")
 
 
-@pytest.mark.parametrize("B,T", [(1, 256), (2, 512), (8, 256), (1, 512)])
+@pytest.mark.parametrize("B,T", [(1, 256), (2, 512), (8, 256), (1, 512), (2, 1024), (1, 2048)])
 def test_forward_kernel_choice(dev, B, T):
     """One shape per head_dim-64 forward kernel the launcher picks by size:
-    split-key (B=1 T=256, B=1 T=512: at most 512 16-query groups), heavy/light
-    pair (B=2 T=512), Q-stationary (B=8 T=256: at least 256 64-query groups);
-    O and LSE against the oracle, the backward at the same shapes too."""
+    split-key (B=1 T=256, B=1 T=512: at most 512 16-query groups; B=2
+    T=1024, B=1 T=2048: long rows, 256..511 64-query groups), heavy/light pair
+    (B=2 T=512), Q-stationary (B=8 T=256: at least 256 64-query groups); O and
+    LSE against the oracle, the backward at the same shapes too."""
     C, H = 768, 12
     x = synth.qkv(B, T, C, seed=5000 + B * T)
     g = synth.grad_out(B, T, C, seed=5000 + B * T)
