@@ -297,6 +297,34 @@ def test_inputs_untouched_and_side_stream(dev):
     assert rel_err(y.cpu().numpy(), yr) <= FWD_RTOL
 
 
+def test_concurrent_streams_get_separate_workspaces(dev):
+    """Backward calls queued on two streams at once (each with its own dS
+    workspace, allocated on first use per stream) give the single-stream
+    results bit for bit, at two sizes so one stream's workspace grows."""
+    import torch
+
+    C, H = 768, 12
+    shapes = [(4, 256), (2, 512)]
+    data = []
+    for B, T in shapes:
+        x = _to(dev, synth.qkv(B, T, C, 77 + T))
+        g = _to(dev, synth.grad_out(B, T, C, 77 + T))
+        y, lse = gpt_amd.attention_forward(x, H)
+        ref_gx, ref_D = gpt_amd.attention_backward(x, y, lse, g, H)
+        data.append((x, g, y, lse, ref_gx, ref_D))
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = []
+    for rep in range(2):
+        for k, st in ((0, s1), (1, s2), (1, s1), (0, s2)):
+            x, g, y, lse, _, _ = data[k]
+            with torch.cuda.stream(st):
+                outs.append((k,) + gpt_amd.attention_backward(x, y, lse, g, H, stream=st))
+    torch.cuda.synchronize()
+    for k, gx, D in outs:
+        assert torch.equal(gx, data[k][4]) and torch.equal(D, data[k][5])
+
+
 def test_batch_slices_are_independent(dev):
     """Running (b, h) slices one at a time gives the batched result."""
     B, T, C, H = 3, 130, 768, 12

@@ -299,6 +299,37 @@ def test_fill_initialisers(dev):
     assert np.all(h[: n - 3] == 1.25) and np.array_equal(h[n - 3:], x[n - 3:].astype(np.float32))
 
 
+def test_concurrent_streams_reductions(dev):
+    """LayerNorm and linear backward (partial-sum workspaces per stream) on two
+    streams at once equal the single-stream results bit for bit."""
+    import torch
+
+    B, T, C, N = 4, 64, 768, 3072
+    r = rng(123)
+    x, gy, gres = (to_dev(dev, f32(r.standard_normal((B, T, C)))) for _ in range(3))
+    mu, var = to_dev(dev, f32(r.standard_normal((B, T)))), to_dev(dev, f32(r.random((B, T)) + 0.5))
+    gam = to_dev(dev, f32(r.standard_normal(C)))
+    w, gyl = to_dev(dev, f32(r.standard_normal((C, N)) * 0.03)), to_dev(dev, f32(r.standard_normal((B, T, N))))
+
+    def run(st):
+        gx, gg, gb = torch.empty_like(x), torch.zeros(C, device=dev), torch.zeros(C, device=dev)
+        ops.device_layernorm_residual_fused_backward(gx, gg, gb, gy, gres, x, mu, var, gam, B, T, C, st)
+        lx, lw, lb = torch.empty_like(x), torch.zeros((C, N), device=dev), torch.zeros(N, device=dev)
+        ops.device_linear_backward(lx, lw, lb, gyl, x, w, B, T, C, N, st)
+        return gx, gg, gb, lx, lw, lb
+
+    ref = [host(t) for t in run(None)]
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(s1):
+        a = run(s1)
+    with torch.cuda.stream(s2):
+        b = run(s2)
+    torch.cuda.synchronize()
+    for out in (a, b):
+        for t, rr in zip(out, ref):
+            assert same_bits(host(t), rr)
+
+
 def test_bad_arguments_are_rejected(dev):
     import torch
 
