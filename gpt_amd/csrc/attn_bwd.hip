@@ -184,7 +184,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     const int J = item / BHc;
     const int bhl = item % BHc, bh = bh0 + bhl;
     const int b = bh / H, h = bh % H;
-    const int kw0 = 64 * J + 16 * w;
+    // Key slice of this wave. The 16-key slices do unequal work on the
+    // diagonal blocks (slice 0 computes 4 of the 16-query halves there, slice
+    // 3 one). When the grid is resident, each SIMD of a CU hosts one wave of
+    // each of the CU's workgroups (c, c + n_cu, c + 2 n_cu), and choosing
+    // the slice by the wave's SIMD with a different table per round evens
+    // the SIMDs' diagonal work (7 or 8 halves each, instead of anything from
+    // 3 to 12 when slices follow wave indices); measured 44.1 -> 43.7 us at
+    // C3, no gain on larger grids, which keep slices = wave indices. The
+    // choice needs the workgroup's 4 waves on 4 different SIMDs, which is
+    // checked through LDS; otherwise slices follow wave indices too.
+    int slice = w;
+    if (n_cu > 0 && (int)gridDim.x <= 3 * n_cu)
+    {
+        __shared__ int sid[4];
+        if (lane == 0)
+            sid[w] = (__builtin_amdgcn_s_getreg(4 | (4 << 6) | (1 << 11))) & 3;  // HW_ID[5:4] = SIMD id
+        lds_barrier();
+        const int simd = sid[w];
+        if (((1 << sid[0]) | (1 << sid[1]) | (1 << sid[2]) | (1 << sid[3])) == 0xF)
+        {
+            // slice per SIMD for rounds 0, 1, 2 (diagonal halves 4, 3, 2, 1 by slice):
+            // per-SIMD sums 4+1+2, 3+2+3, 2+4+1, 1+3+4
+            const int r = (int)blockIdx.x / n_cu;
+            constexpr int kSlice[3][4] = {{0, 1, 2, 3}, {3, 2, 0, 1}, {2, 1, 3, 0}};
+            slice = kSlice[r][simd];
+        }
+    }
+    const int kw0 = 64 * J + 16 * slice;
     const uint32_t Wb = 12u * (uint32_t)C, Cb = 4u * (uint32_t)C, Hb = 4u * (uint32_t)H;
     const rsrc_t rq = make_rsrc(qkv + (long)b * T * 3L * C + (long)h * 64,
                                 (uint32_t)(((long)T * 3 * C - (long)h * 64) * 4));
