@@ -91,50 +91,21 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(float *__restrict__ grad_
     }
 }
 
-// D rows for head_dim 64: one wave per token row (all H heads), lane l reads
-// float4s l, l + 64, ... of the row; the 16 lanes of one head (one DPP row)
-// sum their products with 4 DPP adds. The loads of up to 4 float4 pairs per lane
-// are all issued before the first sum, so a wave has one memory round trip
-// per 4 heads' worth of row instead of one per 64 lanes' worth.
+// D rows for head_dim 64: D[r, h] = sum over the head's 64 columns of
+// dO * O. The [rows, 64 H] tensors are read as one flat stream of float4s,
+// one per thread: the 16 lanes of a DPP row cover one (row, head) (64
+// columns) and sum their products with 4 DPP adds.
 __global__ __launch_bounds__(256) void bwd_rowdot_d64_kernel(float *__restrict__ Dout,
                                                              const float *__restrict__ dy,
-                                                             const float *__restrict__ y,
-                                                             long rows, int H)
+                                                             const float *__restrict__ y, long n4)
 {
-    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows)
+    const long f = (long)blockIdx.x * 256 + threadIdx.x;  // float4 index; n4 is a multiple of 16
+    if (f >= n4)
         return;
-    const int lane = threadIdx.x & 63;
-    const long C = 64L * H;
-    const float4 *a = reinterpret_cast<const float4 *>(dy + row * C);
-    const float4 *o = reinterpret_cast<const float4 *>(y + row * C);
-    const int n4 = 16 * H;
-    for (int f0 = 0; f0 < n4; f0 += 256)
-    {
-        float4 u[4], v[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-        {
-            const int f = f0 + 64 * k + lane;
-            if (f < n4)  // uniform within each 16-lane group
-            {
-                u[k] = a[f];
-                v[k] = o[f];
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-        {
-            const int f = f0 + 64 * k + lane;
-            if (f < n4)
-            {
-                const float s =
-                    row16_sum(u[k].x * v[k].x + u[k].y * v[k].y + u[k].z * v[k].z + u[k].w * v[k].w);
-                if ((lane & 15) == 0)
-                    Dout[row * H + (f >> 4)] = s;
-            }
-        }
-    }
+    const float4 u = reinterpret_cast<const float4 *>(dy)[f], v = reinterpret_cast<const float4 *>(y)[f];
+    const float s = row16_sum(u.x * v.x + u.y * v.y + u.z * v.z + u.w * v.w);
+    if ((threadIdx.x & 15) == 0)
+        Dout[f >> 4] = s;
 }
 
 // Offset (floats) of dS tile (i, j), j <= i, inside one (b, h)'s workspace.
@@ -818,8 +789,8 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
 {
     const long rows = (long)s.B * s.T;
     timer_begin(kKindRowdot, st);
-    hipLaunchKernelGGL(bwd_rowdot_d64_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, D, dy, y,
-                       rows, s.H);
+    const long n4 = rows * 16L * s.H;
+    hipLaunchKernelGGL(bwd_rowdot_d64_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, D, dy, y, n4);
     timer_end(st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
