@@ -11,9 +11,10 @@ value = algorithmic FLOPs / GPU time, FLOPs = 12 * 7 * B * H * d * T * (T+1)
 including the diagonal; exp and masking not counted).
 
 Also reported:
-  kernels       per-kernel average durations over the timed region, from the
-                library's launch timer (a HIP event pair recorded on the launch
-                stream around every kernel, gpt_hip_attn_timing_*)
+  kernels       per-kernel average durations over a second pass of the same
+                steps, from the library's launch timer (gpt_hip_attn_timing_*:
+                each head_dim-64 kernel launched by hipExtLaunchKernelGGL with
+                an event pair that the dispatch's own start and end set)
   roofline      the dominant kernel (most GPU time): algorithmic FLOPs per
                 launch / its average launch duration, against 157.3 TFLOP/s;
                 `traffic` = its measured HBM bytes per launch, read from
@@ -553,7 +554,8 @@ def main():
     total_ms = start.elapsed_time(end)
 
     # Breakdown pass: the same K steps again with an event pair around every op
-    # (torch events) and every kernel launch (the library's launch timer).
+    # (torch events) and the dispatch timestamps of every kernel launch (the
+    # library's launch timer).
     # Kept out of the timed region because the extra event packets between
     # back-to-back kernels slow the step down by ~10%.
     mk = lambda: [torch.cuda.Event(enable_timing=True) for _ in range(LAYERS)]  # noqa: E731

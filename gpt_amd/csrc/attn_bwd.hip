@@ -788,10 +788,8 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
                           const float *qkv, float *ws, int bh_per_chunk, const Shape &s, hipStream_t st)
 {
     const long rows = (long)s.B * s.T;
-    timer_begin(kKindRowdot, st);
     const long n4 = rows * 16L * s.H;
-    hipLaunchKernelGGL(bwd_rowdot_d64_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, D, dy, y, n4);
-    timer_end(st);
+    launch_timed(kKindRowdot, bwd_rowdot_d64_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), st, D, dy, y, n4);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
@@ -801,16 +799,11 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
     for (int bh0 = 0; bh0 < BH; bh0 += bh_per_chunk)
     {
         const int cnt = BH - bh0 < bh_per_chunk ? BH - bh0 : bh_per_chunk;
-        timer_begin(kKindDkdv, st);
-        hipLaunchKernelGGL(bwd_dkdv_d64_kernel, dim3((unsigned)((long)((s.T + 63) / 64) * cnt)), dim3(256), 0, st,
-                           grad_x, ws, lse, D, dy, qkv, s.T, s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale,
-                           cu_count());
-        timer_end(st);
+        launch_timed(kKindDkdv, bwd_dkdv_d64_kernel, dim3((unsigned)((long)((s.T + 63) / 64) * cnt)), dim3(256), st,
+                     grad_x, ws, lse, D, dy, qkv, s.T, s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale, cu_count());
         const unsigned dq_blocks = (unsigned)((long)((n_qb + 1) / 2) * cnt);  // one workgroup per pair
-        timer_begin(kKindDq, st);
-        hipLaunchKernelGGL(bwd_dq_d64_kernel, dim3(dq_blocks), dim3(256), 0, st, grad_x, ws, qkv, s.T, s.C, s.H,
-                           bh0, cnt, n_qb, scale);
-        timer_end(st);
+        launch_timed(kKindDq, bwd_dq_d64_kernel, dim3(dq_blocks), dim3(256), st, grad_x, ws, qkv, s.T, s.C, s.H,
+                     bh0, cnt, n_qb, scale);
         e = hipGetLastError();
         if (e != hipSuccess)
             return e;

@@ -65,10 +65,12 @@ int check_device(const char *op)
     return 0;
 }
 
-// Optional launch timer: when enabled, each kernel launch is bracketed by two
-// HIP events recorded on its stream (from a fixed pool, reused after every
-// read); gpt_hip_attn_timing_read() waits for them and sums the elapsed time
-// per kernel kind. Not thread-safe; meant for one benchmarking thread.
+// Optional launch timer: when enabled, each head_dim-64 kernel launch takes
+// two HIP events (from a fixed pool, reused after every read) that
+// hipExtLaunchKernelGGL sets from the dispatch's start and end; the other
+// launches are bracketed by two events recorded on their stream.
+// gpt_hip_attn_timing_read() waits for them and sums the elapsed time per
+// kernel kind. Not thread-safe; meant for one benchmarking thread.
 constexpr int kTimerSlots = 8192;
 struct LaunchTimer
 {
@@ -163,6 +165,19 @@ void timer_end(hipStream_t st)
         return;
     (void)hipEventRecord(t.ev1[t.open], st);
     t.open = -1;
+}
+
+bool timer_slot(int kind, hipEvent_t *e0, hipEvent_t *e1)
+{
+    LaunchTimer &t = g_timer;
+    *e0 = *e1 = nullptr;
+    if (!t.on || t.used >= kTimerSlots)
+        return false;
+    const int i = t.used++;
+    t.kind[i] = kind;
+    *e0 = t.ev0[i];
+    *e1 = t.ev1[i];
+    return true;
 }
 
 }  // namespace gpt_attn

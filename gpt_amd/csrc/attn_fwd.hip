@@ -895,7 +895,6 @@ hipError_t launch_fwd_d64(float *y, float *lse, const float *qkv, const Shape &s
         nw >>= 1;
     if (n_qb == 1)
         nw = 1;
-    timer_begin(kKindFwd, st);
     const int n_qg = (s.T + 63) / 64;
     const int n_g = (s.T + 15) / 16;
     const long groups = (long)n_qg * BH;
@@ -909,9 +908,8 @@ hipError_t launch_fwd_d64(float *y, float *lse, const float *qkv, const Shape &s
     if (groups >= 256 && !long_rows)
     {
         // enough 64-query groups to fill the GPU: the Q-stationary kernel
-        hipLaunchKernelGGL(fwd_qs_d64_kernel, dim3((unsigned)groups), dim3(256), 0, st, y, lse, qkv, s.T, s.C, s.H,
-                           BH, n_qg, c2, fwd_cu_count());
-        timer_end(st);
+        launch_timed(kKindFwd, fwd_qs_d64_kernel, dim3((unsigned)groups), dim3(256), st, y, lse, qkv, s.T, s.C, s.H,
+                     BH, n_qg, c2, fwd_cu_count());
         return hipGetLastError();
     }
     if (long_rows || (long)n_g * BH <= 512)
@@ -930,35 +928,33 @@ hipError_t launch_fwd_d64(float *y, float *lse, const float *qkv, const Shape &s
         switch (sw)
         {
         case 8:
-            hipLaunchKernelGGL(fwd_split_d64_kernel<8>, g2, dim3(512), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_g, c2);
+            launch_timed(kKindFwd, fwd_split_d64_kernel<8>, g2, dim3(512), st, y, lse, qkv, s.T, s.C, s.H, BH, n_g, c2);
             break;
         case 4:
-            hipLaunchKernelGGL(fwd_split_d64_kernel<4>, g2, dim3(256), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_g, c2);
+            launch_timed(kKindFwd, fwd_split_d64_kernel<4>, g2, dim3(256), st, y, lse, qkv, s.T, s.C, s.H, BH, n_g, c2);
             break;
         case 2:
-            hipLaunchKernelGGL(fwd_split_d64_kernel<2>, g2, dim3(128), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_g, c2);
+            launch_timed(kKindFwd, fwd_split_d64_kernel<2>, g2, dim3(128), st, y, lse, qkv, s.T, s.C, s.H, BH, n_g, c2);
             break;
         default:
-            hipLaunchKernelGGL(fwd_split_d64_kernel<1>, g2, dim3(64), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_g, c2);
+            launch_timed(kKindFwd, fwd_split_d64_kernel<1>, g2, dim3(64), st, y, lse, qkv, s.T, s.C, s.H, BH, n_g, c2);
             break;
         }
-        timer_end(st);
         return hipGetLastError();
     }
     const dim3 grid((unsigned)blocks);
     switch (nw)
     {
     case 4:
-        hipLaunchKernelGGL(fwd_d64_kernel<4>, grid, dim3(256), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_qb, c2);
+        launch_timed(kKindFwd, fwd_d64_kernel<4>, grid, dim3(256), st, y, lse, qkv, s.T, s.C, s.H, BH, n_qb, c2);
         break;
     case 2:
-        hipLaunchKernelGGL(fwd_d64_kernel<2>, grid, dim3(128), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_qb, c2);
+        launch_timed(kKindFwd, fwd_d64_kernel<2>, grid, dim3(128), st, y, lse, qkv, s.T, s.C, s.H, BH, n_qb, c2);
         break;
     default:
-        hipLaunchKernelGGL(fwd_d64_kernel<1>, grid, dim3(64), 0, st, y, lse, qkv, s.T, s.C, s.H, BH, n_qb, c2);
+        launch_timed(kKindFwd, fwd_d64_kernel<1>, grid, dim3(64), st, y, lse, qkv, s.T, s.C, s.H, BH, n_qb, c2);
         break;
     }
-    timer_end(st);
     return hipGetLastError();
 }
 

@@ -2,6 +2,7 @@
 // argument validation). Each returns the hipError_t of its launches.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
@@ -27,6 +28,24 @@ enum KernelKind
 // timer is enabled; no-ops otherwise.
 void timer_begin(int kind, hipStream_t st);
 void timer_end(hipStream_t st);
+
+// Takes a timer slot for one launch of `kind` when the timer is enabled and
+// returns its two events; false (and null events) otherwise.
+bool timer_slot(int kind, hipEvent_t *e0, hipEvent_t *e1);
+
+// One kernel launch; with the timer enabled the slot's events go to
+// hipExtLaunchKernelGGL, which sets them from the dispatch's own start and end
+// timestamps, so the timed span is the kernel alone (no launch gap, no event
+// packets between kernels).
+template <typename K, typename... Args>
+inline void launch_timed(int kind, K kernel, dim3 grid, dim3 block, hipStream_t st, Args... args)
+{
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (timer_slot(kind, &e0, &e1))
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, st, e0, e1, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, 0, st, args...);
+}
 
 // Largest dS workspace one backward call asks for; bigger problems are
 // processed in chunks of (b, h) pairs that fit.

@@ -84,8 +84,10 @@ const char *gpt_hip_attn_last_error(void);
 int gpt_hip_attn_device_ok(void);
 
 /* Launch timer, for benchmarks and tracing. gpt_hip_attn_timing_enable(1)
- * makes every later kernel launch of the library record a HIP event pair on
- * its stream (up to 8192 launches between reads); (0) turns it off.
+ * makes every later kernel launch of the library time itself with a HIP event
+ * pair (head_dim-64 kernels: events set from the dispatch's own start and end
+ * timestamps; others: events recorded on the stream around the launches), up
+ * to 8192 launches between reads; (0) turns it off.
  * gpt_hip_attn_timing_read() waits for the recorded events, writes the summed
  * milliseconds and the launch count per kernel kind into ms[k] / count[k] for
  * k < n_kinds, forgets the recorded launches and returns how many there were.
