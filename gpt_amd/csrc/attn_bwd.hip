@@ -9,23 +9,24 @@
 //   dQ_i  = sum_j dS_ij k_j,  dK_j = sum_i dS_ij q_i,  dV_j = sum_i P_ij dO_i
 // grad_x is overwritten (dQ | dK | dV in the qkv layout) and D is written.
 //
-// head_dim 64 path: deterministic, three launches, no atomics, no memset.
-// Work unit = one 32-query block i x one 32-key block j with j <= i.
-//   bwd_rowdot_d64_kernel  D rows; one wave per token row, 16 lanes per head.
-//   bwd_dkdv_d64_kernel    one workgroup per (b, h, key block j); its NW waves
-//                          split the query blocks i >= j (wave w takes
-//                          j + w, j + w + NW, ...). Per unit, on
-//                          v_mfma_f32_32x32x2_f32:
+// head_dim 64 path: deterministic, no atomics, no memset; two launches up to
+// T = 256, three beyond. Work unit = one 32-query block i x one 32-key block
+// j with j <= i.
+//   bwd_rowdot_d64_kernel  (T > 256) D rows, one float4 per thread, 16 lanes
+//                          per (row, head).
+//   bwd_dkdv_d64_kernel    one workgroup per (b, h, 64-key group); each of its
+//                          4 waves keeps 16 keys' K, V rows in registers and
+//                          walks the query blocks i >= its group on
+//                          v_mfma_f32_16x16x4_f32:
 //                            S  = Q K^T, dP = dO V^T   (queries x keys)
 //                            P = 2^(S c - L), dS = P (dP - D)
-//                            dV += P^T dO, dK += dS^T Q (the S / dP
-//                              accumulators are the A operands as they are)
-//                          and the dS tile is stored to a workspace. The NW
-//                          partial dK, dV are summed through LDS in a fixed
-//                          order and written once with plain stores.
-//   bwd_dq_d64_kernel      one wave per (b, h, heavy/light query-block pair):
-//                          dQ_i = sum_{j<=i} dS_ij K_j from the workspace,
-//                          written once with plain stores.
+//                            dV += P^T dO, dK += dS^T Q
+//                          stores its part of the dS tiles to a workspace and
+//                          writes its dK, dV rows once (nothing to reduce).
+//                          Up to T = 256 it also computes the D rows.
+//   bwd_dq_d64_kernel      one workgroup per (b, h, heavy/light query-block
+//                          pair): dQ_i = sum_{j<=i} dS_ij K_j from the
+//                          workspace on v_mfma_f32_32x32x2_f32, written once.
 // Materialising dS costs 4 KiB of workspace per unit (28 MiB per layer at
 // B=16, T=256, H=12), written and read once; in exchange no dQ element is
 // accumulated by more than one wave, the result is bitwise reproducible, and
@@ -126,10 +127,11 @@ __device__ __forceinline__ long ds_tile(int i, int j) { return ((long)i * (i + 1
 //                                            operands as they are; 4 d-tiles)
 // and the wave's 32 x 16 half of dS tile (i, kw0 / 32) is stored. Workgroups
 // are ordered key-group-major (heaviest first), (b, h) fastest.
+template <bool FUSE_D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void bwd_dkdv_d64_kernel(
     float *__restrict__ grad_x, float *__restrict__ dsw, const float *__restrict__ lse,
-    const float *__restrict__ Dv, const float *__restrict__ dy, const float *__restrict__ qkv, int T, int C, int H,
-    int bh0, int BHc, int n_qb, float c2, float scale, int n_cu)
+    float *__restrict__ Dv, const float *__restrict__ dy, const float *__restrict__ y, const float *__restrict__ qkv,
+    int T, int C, int H, int bh0, int BHc, int n_qb, float c2, float scale, int n_cu)
 {
     constexpr int ST = kTileRow;
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
@@ -188,22 +190,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                                 (uint32_t)(((long)T * 3 * C - (long)h * 64) * 4));
     const rsrc_t ro = make_rsrc(dy + (long)b * T * C + (long)h * 64, (uint32_t)(((long)T * C - (long)h * 64) * 4));
     const rsrc_t rl = make_rsrc(lse + (long)b * T * H + h, (uint32_t)(((long)T * H - h) * 4));
+    const rsrc_t ry = make_rsrc(y + (long)b * T * C + (long)h * 64, (uint32_t)(((long)T * C - (long)h * 64) * 4));
     const rsrc_t rd = make_rsrc(Dv + (long)b * T * H + h, (uint32_t)(((long)T * H - h) * 4));
     float *ws = dsw + (long)bhl * ((long)n_qb * (n_qb + 1) / 2) * 1024;
     float *gx = grad_x + (long)b * T * 3L * C + (long)h * 64;
 
-    // Q, dO of the block, swizzled (tile_off), and its lse (0..31) and D
-    // (64..95) rows; one array per buffer, so that the compiler sees that
-    // loads landing in one buffer do not alias reads of the other
-    __shared__ __attribute__((aligned(16))) float sq0[32 * ST], so0[32 * ST], sld0[128];
-    __shared__ __attribute__((aligned(16))) float sq1[32 * ST], so1[32 * ST], sld1[128];
+    // Q, dO of the block, swizzled (tile_off), with FUSE_D O of the block
+    // (laid out as dO, read only by the lane that staged it), and its lse
+    // (0..31) and D (64..95) rows; one array per buffer, so that the compiler
+    // sees that loads landing in one buffer do not alias reads of the other
+    constexpr int YT = FUSE_D ? 32 * ST : 4;
+    __shared__ __attribute__((aligned(16))) float sq0[32 * ST], so0[32 * ST], sy0[YT], sld0[128];
+    __shared__ __attribute__((aligned(16))) float sq1[32 * ST], so1[32 * ST], sy1[YT], sld1[128];
     auto bufs = [&](auto buf_c) {
         constexpr int buf = decltype(buf_c)::value;
         struct B
         {
-            float *q, *o, *ld;
+            float *q, *o, *y, *ld;
         };
-        return buf == 0 ? B{sq0, so0, sld0} : B{sq1, so1, sld1};
+        return buf == 0 ? B{sq0, so0, sy0, sld0} : B{sq1, so1, sy1, sld1};
     };
 
     // stationary B operands: lane l holds K / V[kw0 + l%16][16 (l/16) + m],
@@ -232,7 +237,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     // 4k .. 4k + 3; wave w moves chunks w and w + 4 of Q and of dO. Lane l
     // lands at row 4k + l/16, physical column group l%16, so it fetches the
     // logical group (l%16) ^ tile_swz(row), tile_swz(row) = (l/16) << 2 | w for
-    // both of its chunks. Wave 0 also moves the lse and D rows of the block.
+    // both of its chunks. With FUSE_D, O moves like dO (for the D rows);
+    // otherwise wave 0 moves the block's D rows (from bwd_rowdot_d64_kernel).
+    // Wave 0 also moves the lse rows of the block.
     const uint32_t dma_row = (uint32_t)(4 * w + (lane >> 4));
     const uint32_t dma_col = 16u * (uint32_t)((lane & 15) ^ (((lane >> 4) << 2) | w));
     const uint32_t dq_lane = dma_row * Wb + dma_col, do_lane = dma_row * Cb + dma_col;
@@ -246,11 +253,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
         dma16(rq, B.q + 256 * (w + 4), dq_lane + 16u * Wb, qo);
         dma16(ro, B.o + 256 * w, do_lane, oo);
         dma16(ro, B.o + 256 * (w + 4), do_lane + 16u * Cb, oo);
+        if constexpr (FUSE_D)
+        {
+            dma16(ry, B.y + 256 * w, do_lane, oo);
+            dma16(ry, B.y + 256 * (w + 4), do_lane + 16u * Cb, oo);
+        }
         if (w == 0)
         {
             const uint32_t lo = ok ? 32u * (uint32_t)i * Hb : kNoBlock;
             dma4(rl, B.ld, ld_lane, lo);
-            dma4(rd, B.ld + 64, ld_lane, lo);
+            if constexpr (!FUSE_D)
+                dma4(rd, B.ld + 64, ld_lane, lo);
+        }
+    };
+    // D rows of block i, D = rowsum(dO * O), once its staging has landed:
+    // each lane multiplies the dO and O float4s it staged itself (rows
+    // 4 w + l/16 and 16 + 4 w + l/16, so no barrier is needed before the
+    // reads), the 16 lanes of a row add them up, and the row's lane 0 writes
+    // D into the buffer's D rows (made visible by the barrier that ends the
+    // step). Every workgroup of a (b, h) computes a block's D the same way;
+    // the one whose first two blocks include it (J = i / 2) also stores it.
+    auto d_rows = [&](const int i, auto buf_c) {
+        const auto B = bufs(buf_c);
+        float dsum[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+        {
+            const float4 o = *reinterpret_cast<const float4 *>(B.o + 256 * (w + 4 * k) + 4 * lane);
+            const float4 u = *reinterpret_cast<const float4 *>(B.y + 256 * (w + 4 * k) + 4 * lane);
+            dsum[k] = row16_sum(o.x * u.x + o.y * u.y + o.z * u.z + o.w * u.w);
+        }
+        if ((lane & 15) == 0)
+        {
+            const int r0 = 4 * w + (lane >> 4);
+            B.ld[64 + r0] = dsum[0];
+            B.ld[80 + r0] = dsum[1];
+            if (i <= 2 * J + 1)
+            {
+                const int q = 32 * i + r0;
+                if (q < T)
+                    Dv[((long)b * T + q) * H + h] = dsum[0];
+                if (q + 16 < T)
+                    Dv[((long)b * T + q + 16) * H + h] = dsum[1];
+            }
         }
     };
 
@@ -259,6 +304,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     const int i_lo = 2 * J;
     issue(i_lo, BufIdx<0>{});
     lds_dma_wait();
+    if constexpr (FUSE_D)
+        d_rows(i_lo, BufIdx<0>{});
     __syncthreads();
     // One query block; the LDS buffer index is a compile-time constant (the
     // loop below is unrolled by two) so that it folds into the ds_read offsets.
@@ -435,6 +482,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
             }
             __builtin_amdgcn_sched_barrier(0);
             vm_wait<8>();
+        }
+        if constexpr (FUSE_D)
+        {
+            if (i + 1 < n_qb)
+                d_rows(i + 1, BufIdx<buf ^ 1>{});
         }
         lds_barrier();
     };
@@ -787,20 +839,35 @@ static int cu_count()
 hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
                           const float *qkv, float *ws, int bh_per_chunk, const Shape &s, hipStream_t st)
 {
-    const long rows = (long)s.B * s.T;
-    const long n4 = rows * 16L * s.H;
-    launch_timed(kKindRowdot, bwd_rowdot_d64_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), st, D, dy, y, n4);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess)
-        return e;
+    // D rows inside the dK/dV kernel while few key groups recompute a block's
+    // D (T <= 256: at most 4): one launch less, measured backward 70.9 ->
+    // 68.2 us at B=16 T=256, 37.2 -> 35.9 us at B=1 T=256; at T = 512 the
+    // two ways measure the same and at T = 4096 (64 key groups) the separate
+    // D-row pass is as fast or faster, so longer rows keep it.
+    const bool fuse_d = s.T <= 256;
+    hipError_t e = hipSuccess;
+    if (!fuse_d)
+    {
+        const long n4 = (long)s.B * s.T * 16L * s.H;
+        launch_timed(kKindRowdot, bwd_rowdot_d64_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), st, D, dy, y,
+                     n4);
+        e = hipGetLastError();
+        if (e != hipSuccess)
+            return e;
+    }
     const int n_qb = (s.T + 31) / 32;
     const int BH = s.B * s.H;
     const float scale = softmax_scale(64);
     for (int bh0 = 0; bh0 < BH; bh0 += bh_per_chunk)
     {
         const int cnt = BH - bh0 < bh_per_chunk ? BH - bh0 : bh_per_chunk;
-        launch_timed(kKindDkdv, bwd_dkdv_d64_kernel, dim3((unsigned)((long)((s.T + 63) / 64) * cnt)), dim3(256), st,
-                     grad_x, ws, lse, D, dy, qkv, s.T, s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale, cu_count());
+        const dim3 g((unsigned)((long)((s.T + 63) / 64) * cnt));
+        if (fuse_d)
+            launch_timed(kKindDkdv, bwd_dkdv_d64_kernel<true>, g, dim3(256), st, grad_x, ws, lse, D, dy, y, qkv, s.T,
+                         s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale, cu_count());
+        else
+            launch_timed(kKindDkdv, bwd_dkdv_d64_kernel<false>, g, dim3(256), st, grad_x, ws, lse, D, dy, y, qkv,
+                         s.T, s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale, cu_count());
         const unsigned dq_blocks = (unsigned)((long)((n_qb + 1) / 2) * cnt);  // one workgroup per pair
         launch_timed(kKindDq, bwd_dq_d64_kernel, dim3(dq_blocks), dim3(256), st, grad_x, ws, qkv, s.T, s.C, s.H,
                      bh0, cnt, n_qb, scale);

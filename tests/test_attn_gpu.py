@@ -122,7 +122,9 @@ def test_forward_kernel_choice(dev, B, T):
     split-key (B=1 T=256, B=1 T=512: at most 512 16-query groups; B=2
     T=1024, B=1 T=2048: long rows, 256..511 64-query groups), heavy/light pair
     (B=2 T=512), Q-stationary (B=8 T=256: at least 256 64-query groups); O and
-    LSE against the oracle, the backward at the same shapes too."""
+    LSE against the oracle, the backward at the same shapes too (its D rows
+    inside the dK/dV kernel up to T = 256, from the separate D-row kernel
+    beyond)."""
     C, H = 768, 12
     x = synth.qkv(B, T, C, seed=5000 + B * T)
     g = synth.grad_out(B, T, C, seed=5000 + B * T)
@@ -335,10 +337,13 @@ def test_batch_slices_are_independent(dev):
         assert np.array_equal(yb, y[b:b + 1]) and np.array_equal(lb, lse[b:b + 1])
 
 
-def test_launch_timer_counts_each_kernel(dev):
+@pytest.mark.parametrize("T", [100, 300])
+def test_launch_timer_counts_each_kernel(dev, T):
+    """One launch per kernel; up to T = 256 the dK/dV kernel computes the D
+    rows itself, longer rows take the separate D-row kernel."""
     import torch
 
-    B, T, C, H = 2, 100, 768, 12
+    B, C, H = 2, 768, 12
     x = _to(dev, synth.qkv(B, T, C, 51))
     g = _to(dev, synth.grad_out(B, T, C, 51))
     gpt_amd.timing_enable(True)
@@ -349,8 +354,9 @@ def test_launch_timer_counts_each_kernel(dev):
         t = gpt_amd.timing_read()
     finally:
         gpt_amd.timing_enable(False)
-    for k in ("fwd", "bwd_rowdot", "bwd_dkdv", "bwd_dq"):
+    for k in ("fwd", "bwd_dkdv", "bwd_dq"):
         ms, n = t[k]
         assert n == 1 and ms > 0, (k, t[k])
+    assert t["bwd_rowdot"][1] == (0 if T <= 256 else 1), t
     assert t["other"] == (0.0, 0)
     assert gpt_amd.timing_read()["fwd"] == (0.0, 0)  # read forgets
