@@ -91,7 +91,8 @@ int gpt_hip_attn_device_ok(void);
  * gpt_hip_attn_timing_read() waits for the recorded events, writes the summed
  * milliseconds and the launch count per kernel kind into ms[k] / count[k] for
  * k < n_kinds, forgets the recorded launches and returns how many there were.
- * Kinds: 0 head_dim-64 forward, 1 backward D rows, 2 backward dK/dV (+ dS
+ * Kinds: 0 head_dim-64 forward, 1 backward D rows (T > 256; up to T = 256
+ * the dK/dV kernel computes them), 2 backward dK/dV (+ dS
  * tiles), 3 backward dQ, 4 everything else (general-d kernels, the atomic
  * variant). Not thread-safe. No reference counterpart (the reference times
  * whole training steps with a host clock, src/core/benchmark.h:5-16). */
