@@ -37,6 +37,15 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // take the general-d kernels.
 bool slice_fits_buffer(const gpt_attn::Shape &s) { return (long long)s.T * 3LL * s.C * 4LL < (1LL << 31); }
 
+// The head_dim-64 backward reads one (b, h)'s dS tiles through a buffer range
+// too: n (n + 1) / 2 tiles of 4 KiB for n = ceil(T / 32) query blocks, below
+// 2^31 bytes up to T = 32736. Longer rows take the general-d kernels.
+bool ds_fits_buffer(const gpt_attn::Shape &s)
+{
+    const long long n = (s.T + 31) / 32;
+    return n * (n + 1) / 2 * 4096LL < (1LL << 31);
+}
+
 int check_shape(const char *op, int B, int T, int C, int H, gpt_attn::Shape *s)
 {
     if (B < 0 || T < 0 || C <= 0 || H <= 0)
@@ -221,8 +230,8 @@ int gpt_hip_attn_bwd_f32(float *grad_x, float *D_cache, const float *lse, const 
     if (int rc = check_device(op))
         return rc;
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const bool mfma = g_path != 1 && s.d == 64 && slice_fits_buffer(s) && aligned16(grad_x) &&
-                      aligned16(grad_y) && aligned16(y) && aligned16(qkv);
+    const bool mfma = g_path != 1 && s.d == 64 && slice_fits_buffer(s) && ds_fits_buffer(s) &&
+                      aligned16(grad_x) && aligned16(grad_y) && aligned16(y) && aligned16(qkv);
     if (!mfma)
     {
         const hipError_t e = gpt_attn::launch_bwd_general(grad_x, D_cache, lse, grad_y, y, qkv, s, st);

@@ -101,7 +101,9 @@ int gpt_hip_attn_timing_read(double *ms, int *count, int n_kinds);
 
 /* Kernel selection, for tests and tuning only (not thread-safe; process-wide).
  *   path 0  automatic (default): MFMA kernels for head_dim 64, general-d
- *           kernels otherwise
+ *           kernels otherwise and for head_dim-64 calls beyond the MFMA
+ *           kernels' 32-bit buffer ranges (T * 3 * hidden_size * 4 bytes
+ *           per batch slice >= 2^31; backward also T > 32736)
  *   path 1  always the general-d kernels (a second, independent HIP
  *           implementation used to cross-check the MFMA kernels)
  *   path 2  as 0, but the head_dim-64 backward accumulates dQ with fp32

@@ -252,6 +252,61 @@ def test_config5a_B2_T4096(dev):
     _slices_and_invariants(dev, x, g, H, [(0, 0), (1, 11)], "C5a")
 
 
+@pytest.mark.parametrize("T", [32736, 32800])
+def test_longest_rows_single_head(dev, T):
+    """Maximum sequence length of the head_dim-64 backward: at T = 32736 one
+    (b, h)'s dS tiles (523776 x 4 KiB) stay just below the 2^31-byte buffer
+    range the dQ kernel reads them through; at T = 32800 the call takes the
+    general-d kernels. B=1, H=1, d=64 (the oracle would take hours here):
+    O, LSE and dQ at sampled rows, dK and dV at keys 0 and T - 1 and D
+    everywhere against float64 numpy (dQ, dK_0 and dV_0 from the kernels' own
+    LSE and D, which are checked first), plus the size-independent invariants."""
+    B, C, H, d = 1, 64, 1, 64
+    x = synth.qkv(B, T, C, seed=777)
+    g = synth.grad_out(B, T, C, seed=777)
+    gpt_amd.timing_enable(True)
+    try:
+        y, lse = gpu_fwd(dev, x, H)
+        gx, D = gpu_bwd(dev, x, y, lse, g, H)
+        t = gpt_amd.timing_read()
+    finally:
+        gpt_amd.timing_enable(False)
+    assert t["bwd_dkdv"][1] == (1 if T <= 32736 else 0), t
+    assert t["other"][1] == (0 if T <= 32736 else 1), t  # the forward stays on the MFMA kernels
+    assert np.all(np.isfinite(y)) and np.all(np.isfinite(lse)) and np.all(np.isfinite(gx))
+    q, k, v = (x[0, :, i * C:(i + 1) * C].astype(np.float64) for i in range(3))
+    go = g[0].astype(np.float64)
+    sc = 1.0 / np.sqrt(d)
+    L = lse[0, :, 0].astype(np.float64)
+    rows = (0, 1, 4095, T // 2, T - 2, T - 1)
+    dq, dq_ref = [], []
+    for i in rows:
+        s = q[i] @ k[:i + 1].T * sc
+        lr = np.logaddexp.reduce(s)
+        p = np.exp(s - lr)
+        assert_close(f"T={T} O[{i}]", y[0, i], p @ v[:i + 1], FWD_RTOL)
+        assert abs(L[i] - lr) <= FWD_RTOL * max(1.0, abs(lr)), (i, L[i], lr)
+        pk = np.exp(s - L[i])
+        ds = pk * (go[i] @ v[:i + 1].T - D[0, i, 0]) * sc
+        dq.append(gx[0, i, :C])
+        dq_ref.append(ds @ k[:i + 1])
+    # row-wise norms: dQ_0 is zero up to rounding (dS_00 = dO_0 . v_0 - D_0 = 0)
+    assert_close(f"T={T} dQ{rows}", np.stack(dq), np.stack(dq_ref), BWD_RTOL)
+    assert_close(f"T={T} D", D[0, :, 0], np.sum(go * y[0].astype(np.float64), axis=1), BWD_RTOL)
+    # key 0 sees every query, key T - 1 only the last
+    p0 = np.exp(q @ k[0] * sc - L)
+    assert_close(f"T={T} dV[0]", gx[0, 0, 2 * C:], p0 @ go, BWD_RTOL)
+    ds0 = p0 * (go @ v[0] - D[0, :, 0].astype(np.float64)) * sc
+    assert_close(f"T={T} dK[0]", gx[0, 0, C:2 * C], ds0 @ q, BWD_RTOL)
+    pl = np.exp(q[T - 1] @ k[T - 1] * sc - L[T - 1])
+    assert_close(f"T={T} dV[T-1]", gx[0, T - 1, 2 * C:], pl * go[T - 1], BWD_RTOL)
+    dsl = pl * (go[T - 1] @ v[T - 1] - D[0, T - 1, 0]) * sc
+    assert_close(f"T={T} dK[T-1]", gx[0, T - 1, C:2 * C], dsl * q[T - 1], BWD_RTOL)
+    dk = gx[0, :, C:2 * C].astype(np.float64)
+    assert np.abs(dk.sum(0)).max() <= 1e-4 * np.abs(dk).max() * np.sqrt(T)
+    assert rel_err(gx[0, :, 2 * C:].astype(np.float64).sum(0), go.sum(0)) <= 1e-4
+
+
 def test_backward_overwrites_grad_x_and_is_repeatable(dev):
     import torch
 
