@@ -10,6 +10,7 @@
 #include "ops_internal.h"
 
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
 
@@ -18,6 +19,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <string>
 
 namespace {
 
@@ -171,6 +173,63 @@ int ws_get(const char *op, float **out, size_t floats, hipStream_t st, int slot 
 
 // ---------------------------------------------------------------- hipBLASLt
 
+// Tuned hipBLASLt kernels for the GPT-2 124M linear layers at B T = 4096
+// rows (row-major shapes as issued below: forward x w + b, grad_x = grad_y
+// w^T, grad_w += x^T grad_y). For each shape, every workspace-free candidate
+// among the heuristic's first 32 was timed on MI355X (random fp32 data,
+// median of 10 calls, two runs agreeing) and the fastest kept, named by the
+// 64-bit FNV-1a hash of its kernel name (solution indices are not stable
+// from one process to the next; kernel names are). The plan takes that
+// kernel when the heuristic offers it, else the heuristic's first choice,
+// which is also what happens with a hipBLASLt build other than ROCm 7.2's.
+struct LtTuned
+{
+    bool ta, tb;
+    int M, N, K, epi;
+    unsigned long long kernel;  // FNV-1a 64 of the kernel name
+};
+constexpr LtTuned kLtTuned[] = {
+    // forward with the bias epilogue: qkv (MT192x64x16, 126 -> 108 us),
+    // attention projection (MT96x64x32, 44.2 -> 42.5), FFN up (MT128x128x16,
+    // then this library's GELU pass; 165 -> 137.6), FFN down (MT192x64x32,
+    // 142 -> 137)
+    {false, false, 4096, 2304, 768, 1, 0xf3e165f544abc1d0ull},
+    {false, false, 4096, 768, 768, 1, 0xfc2ab4e5816e54c1ull},
+    {false, false, 4096, 3072, 768, 1, 0xb7031046e884ef98ull},
+    {false, false, 4096, 768, 3072, 1, 0x97d87630ed7dfec3ull},
+    // grad_x: qkv (MT192x32x32, 122 -> 109.5 us), attention projection
+    // (MT128x32x32, 46 -> 43), FFN up (MT96x128x32, 143.5 -> 136.4), FFN down
+    // (MT128x128x16, 154 -> 139; rocBLAS 153.5)
+    {false, true, 4096, 768, 2304, 0, 0x6e3323c1c0733693ull},
+    {false, true, 4096, 768, 768, 0, 0x64e42940d84ef6b5ull},
+    {false, true, 4096, 768, 3072, 0, 0xf1575e4eba18b982ull},
+    {false, true, 4096, 3072, 768, 0, 0x00a8af8e17cf3704ull},
+    // grad_w: qkv (MT32x256x32, 138.7 -> 131 us), attention projection
+    // (MT96x32x128, 133.7 -> 58.8); FFN up and down keep the first choice
+    {true, false, 768, 2304, 4096, 0, 0x966ae45d717321c0ull},
+    {true, false, 768, 768, 4096, 0, 0x262605300ea95f49ull},
+};
+
+// Tuned kernel hash for a GEMM, or 0.
+unsigned long long lt_tuned(bool ta, bool tb, int M, int N, int K, int epi)
+{
+    for (const LtTuned &t : kLtTuned)
+        if (t.ta == ta && t.tb == tb && t.M == M && t.N == N && t.K == K && t.epi == epi)
+            return t.kernel;
+    return 0;
+}
+
+unsigned long long fnv1a64(const std::string &s)
+{
+    unsigned long long h = 1469598103934665603ull;
+    for (const unsigned char c : s)
+    {
+        h ^= c;
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
 // Which library takes a GEMM is a fixed rule (use_lt), from measurements of
 // both on MI355X at the GPT-2 124M step shapes (random fp32 data, M = B T =
 // 4096): hipBLASLt's fp32 kernels win where the row-major product has at
@@ -183,6 +242,9 @@ int ws_get(const char *op, float **out, size_t floats, hipStream_t st, int slot 
 // results are bitwise reproducible. One hipBLASLt plan (descriptor, layouts,
 // heuristic algorithm) per (device, shape, transposes, epilogue), built on
 // first use and kept; rocBLAS takes any shape hipBLASLt has no plan for.
+// Shapes with a tuned kernel (kLtTuned) always go to hipBLASLt: tuned, it
+// beats rocBLAS on the wide ones too (qkv forward 108 vs 122.5 us plus the
+// bias pass; grad_x of FFN down 139 vs 153.5 us).
 struct LtPlan
 {
     int dev;
@@ -250,7 +312,7 @@ LtPlan *lt_plan(int dev, bool ta, bool tb, int M, int N, int K, int lda, int ldb
     // that do were seen to fail at launch with an internal error on some
     // shapes, and their cross-workgroup reductions need not be reproducible.
     size_t wmax = 0;
-    constexpr int kAsk = 8;
+    constexpr int kAsk = 32;
     hipblasLtMatmulHeuristicResult_t res[kAsk];
     int n = 0;
     const bool asked =
@@ -259,17 +321,26 @@ LtPlan *lt_plan(int dev, bool ta, bool tb, int M, int N, int K, int lda, int ldb
     hipblasLtMatmulPreferenceDestroy(pref);
     if (!asked)
         return nullptr;
+    const unsigned long long want = lt_tuned(ta, tb, M, N, K, epi);
+    int pick = -1;
     for (int i = 0; i < n; ++i)
     {
-        if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize == 0)
+        if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize != 0)
+            continue;
+        if (pick < 0)
+            pick = i;  // the heuristic's first workspace-free choice
+        if (want && fnv1a64(hipblaslt_ext::getKernelNameFromAlgo(g_lt[dev], res[i].algo)) == want)
         {
-            q.algo = res[i].algo;
-            q.ws = 0;
-            q.ok = true;
-            return &q;
+            pick = i;
+            break;
         }
     }
-    return nullptr;
+    if (pick < 0)
+        return nullptr;
+    q.algo = res[pick].algo;
+    q.ws = 0;
+    q.ok = true;
+    return &q;
 }
 
 // Row-major C[M x N] = alpha op(A) op(B) + beta C, with the epilogue: epi 1
@@ -305,11 +376,12 @@ int lt_gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int 
 
 bool use_lt(bool ta, int N) { return ta || N <= 1024; }
 
-// Plain GEMM: hipBLASLt where use_lt says so and it has a plan, else rocBLAS.
+// Plain GEMM: hipBLASLt where use_lt says so or a tuned solution exists and
+// it has a plan, else rocBLAS.
 int gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int K, float alpha, const float *A, int lda,
          const float *B, int ldb, float beta, float *C, int ldc)
 {
-    if (use_lt(ta, N))
+    if (use_lt(ta, N) || lt_tuned(ta, tb, M, N, K, 0))
     {
         const int rc = lt_gemm(op, st, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, 0, nullptr, nullptr);
         if (rc != 1)
@@ -467,16 +539,18 @@ int gpt_hip_linear_activation_forward_f32(float *y, float *act, const float *x, 
         return rc;
     const hipStream_t st = as_stream(stream);
     const int M = (int)rows, K = input_size, N = output_size;
-    // y [M x N] = x [M x K] w [K x N] + b. On hipBLASLt (use_lt) the bias goes
-    // in its epilogue, and with activation the GELU too when g_fused_gelu
-    // allows it (D = act, pre-activation y as the auxiliary output), else one
-    // pass of this library's GELU over y. On rocBLAS one pass adds the bias
-    // and writes the GELU.
-    if (!use_lt(false, N))
+    // y [M x N] = x [M x K] w [K x N] + b. On hipBLASLt (use_lt, or a tuned
+    // bias-epilogue solution) the bias goes in its epilogue, and with
+    // activation the GELU too when g_fused_gelu allows it and the shape has no
+    // tuned bias-only solution (D = act, pre-activation y as the auxiliary
+    // output), else one pass of this library's GELU over y. On rocBLAS one
+    // pass adds the bias and writes the GELU.
+    const bool tuned = lt_tuned(false, false, M, N, K, 1) != 0;
+    if (!use_lt(false, N) && !tuned)
     {
         // rocBLAS below
     }
-    else if (activation && g_fused_gelu)
+    else if (activation && g_fused_gelu && !tuned)
     {
         const int rc = lt_gemm(op, st, false, false, M, N, K, 1.f, x, K, w, N, 0.f, act, N, 2, b, y);
         if (rc != 1)
