@@ -179,9 +179,13 @@ int ws_get(const char *op, float **out, size_t floats, hipStream_t st, int slot 
 // among the heuristic's first 32 was timed on MI355X (random fp32 data,
 // median of 10 calls, two runs agreeing) and the fastest kept, named by the
 // 64-bit FNV-1a hash of its kernel name (solution indices are not stable
-// from one process to the next; kernel names are). The plan takes that
-// kernel when the heuristic offers it, else the heuristic's first choice,
-// which is also what happens with a hipBLASLt build other than ROCm 7.2's.
+// from one process to the next; kernel names are). Two hipBLASLt builds are
+// covered: ROCm 7.2's in /opt/rocm, which the reference-side programs load,
+// and the one bundled with PyTorch, which a process that imported torch has
+// already loaded when this library binds libhipblaslt.so.1 (the kernel sets
+// differ). The plan takes the first heuristic candidate whose kernel is in
+// the table for its shape, else the heuristic's first choice; shapes that
+// use_lt would send to rocBLAS go to hipBLASLt only on a table hit.
 struct LtTuned
 {
     bool ta, tb;
@@ -189,17 +193,18 @@ struct LtTuned
     unsigned long long kernel;  // FNV-1a 64 of the kernel name
 };
 constexpr LtTuned kLtTuned[] = {
-    // forward with the bias epilogue: qkv (MT192x64x16, 126 -> 108 us),
-    // attention projection (MT96x64x32, 44.2 -> 42.5), FFN up (MT128x128x16,
-    // then this library's GELU pass; 165 -> 137.6), FFN down (MT192x64x32,
-    // 142 -> 137)
+    // ROCm 7.2 build. Forward with the bias epilogue: qkv (MT192x64x16,
+    // 126 -> 108 us; rocBLAS 122.5 + the bias pass), attention projection
+    // (MT96x64x32, 44.2 -> 42.5), FFN down (MT192x64x32, 142 -> 137). FFN up
+    // stays on rocBLAS + the bias and GELU pass: its best bias-epilogue
+    // kernel here (137.6 us + a GELU pass) would save about 10 us, but an
+    // entry for it made the same call 15 us slower under PyTorch's build.
     {false, false, 4096, 2304, 768, 1, 0xf3e165f544abc1d0ull},
     {false, false, 4096, 768, 768, 1, 0xfc2ab4e5816e54c1ull},
-    {false, false, 4096, 3072, 768, 1, 0xb7031046e884ef98ull},
     {false, false, 4096, 768, 3072, 1, 0x97d87630ed7dfec3ull},
     // grad_x: qkv (MT192x32x32, 122 -> 109.5 us), attention projection
     // (MT128x32x32, 46 -> 43), FFN up (MT96x128x32, 143.5 -> 136.4), FFN down
-    // (MT128x128x16, 154 -> 139; rocBLAS 153.5)
+    // (MT128x128x16, 139; rocBLAS 153.5)
     {false, true, 4096, 768, 2304, 0, 0x6e3323c1c0733693ull},
     {false, true, 4096, 768, 768, 0, 0x64e42940d84ef6b5ull},
     {false, true, 4096, 768, 3072, 0, 0xf1575e4eba18b982ull},
@@ -208,15 +213,37 @@ constexpr LtTuned kLtTuned[] = {
     // (MT96x32x128, 133.7 -> 58.8); FFN up and down keep the first choice
     {true, false, 768, 2304, 4096, 0, 0x966ae45d717321c0ull},
     {true, false, 768, 768, 4096, 0, 0x262605300ea95f49ull},
+    // PyTorch's bundled build. Forward: qkv (MT144x256x32, 150 -> 116 us;
+    // rocBLAS 123 + the bias pass), attention projection (MT192x64x32,
+    // 55-70 -> 47.5), FFN down (MT96x128x32, 154 -> 142); FFN up stays on
+    // rocBLAS (142 + the bias and GELU pass against 147 + the GELU pass)
+    {false, false, 4096, 2304, 768, 1, 0x8c64e1e46bcba5cbull},
+    {false, false, 4096, 768, 768, 1, 0x9dbc1e588c20de9dull},
+    {false, false, 4096, 768, 3072, 1, 0xd72dbb1ca0f664ddull},
+    // grad_x: qkv (MT192x64x32, 135 -> 110.7 us), attention projection (the
+    // same kernel, 51.9 -> 48), FFN up (MT96x128x32, 153 -> 141.5); FFN down
+    // stays on rocBLAS (136 against 147)
+    {false, true, 4096, 768, 2304, 0, 0x5172d33dba3ee5f8ull},
+    {false, true, 4096, 768, 768, 0, 0x5172d33dba3ee5f8ull},
+    {false, true, 4096, 768, 3072, 0, 0x1410995819952b0eull},
+    // grad_w: qkv (MT32x256x32, 144 -> 130.5 us), attention projection
+    // (MT32x96x64, 62.2 -> 60.9), FFN up and down (MT64x160x32, 168 -> 158,
+    // 172-179 -> 156)
+    {true, false, 768, 2304, 4096, 0, 0xa8f15526ba86aa4eull},
+    {true, false, 768, 768, 4096, 0, 0xb66bfddbfc77941cull},
+    {true, false, 768, 3072, 4096, 0, 0x17a86e04fb1d2a39ull},
+    {true, false, 3072, 768, 4096, 0, 0x17a86e04fb1d2a39ull},
 };
 
-// Tuned kernel hash for a GEMM, or 0.
-unsigned long long lt_tuned(bool ta, bool tb, int M, int N, int K, int epi)
+// Whether the table lists `kernel` for this GEMM (kernel 0: whether it lists
+// any kernel for it).
+bool lt_tuned(bool ta, bool tb, int M, int N, int K, int epi, unsigned long long kernel = 0)
 {
     for (const LtTuned &t : kLtTuned)
-        if (t.ta == ta && t.tb == tb && t.M == M && t.N == N && t.K == K && t.epi == epi)
-            return t.kernel;
-    return 0;
+        if (t.ta == ta && t.tb == tb && t.M == M && t.N == N && t.K == K && t.epi == epi &&
+            (kernel == 0 || t.kernel == kernel))
+            return true;
+    return false;
 }
 
 unsigned long long fnv1a64(const std::string &s)
@@ -242,9 +269,10 @@ unsigned long long fnv1a64(const std::string &s)
 // results are bitwise reproducible. One hipBLASLt plan (descriptor, layouts,
 // heuristic algorithm) per (device, shape, transposes, epilogue), built on
 // first use and kept; rocBLAS takes any shape hipBLASLt has no plan for.
-// Shapes with a tuned kernel (kLtTuned) always go to hipBLASLt: tuned, it
-// beats rocBLAS on the wide ones too (qkv forward 108 vs 122.5 us plus the
-// bias pass; grad_x of FFN down 139 vs 153.5 us).
+// A wide shape goes to hipBLASLt too when the loaded build offers the
+// table's kernel for it (kLtTuned): tuned, hipBLASLt beats rocBLAS there
+// (ROCm 7.2: qkv forward 108 vs 122.5 us plus the bias pass; grad_x of FFN
+// down 139 vs 153.5 us).
 struct LtPlan
 {
     int dev;
@@ -252,6 +280,7 @@ struct LtPlan
     int M, N, K, lda, ldb, ldc;
     int epi;  // 0 none, 1 + bias, 2 + bias with GELU (pre-activation to aux)
     bool ok;
+    bool tuned;  // the algorithm is the table's kernel for this shape
     hipblasLtMatmulDesc_t desc;
     hipblasLtMatrixLayout_t la, lb, lc;
     hipblasLtMatmulAlgo_t algo;
@@ -283,7 +312,7 @@ LtPlan *lt_plan(int dev, bool ta, bool tb, int M, int N, int K, int lda, int ldb
         return nullptr;
     }
     LtPlan &q = g_plans[g_nplans++];
-    q = LtPlan{dev, ta, tb, M, N, K, lda, ldb, ldc, epi, false, nullptr, nullptr, nullptr, nullptr, {}, 0};
+    q = LtPlan{dev, ta, tb, M, N, K, lda, ldb, ldc, epi, false, false, nullptr, nullptr, nullptr, nullptr, {}, 0};
     // column-major view: C^T [N x M] = op(B)^T [N x K] op(A)^T [K x M]
     const hipblasOperation_t opa = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N;
     const uint32_t ep = epi == 0 ? HIPBLASLT_EPILOGUE_DEFAULT
@@ -321,7 +350,7 @@ LtPlan *lt_plan(int dev, bool ta, bool tb, int M, int N, int K, int lda, int ldb
     hipblasLtMatmulPreferenceDestroy(pref);
     if (!asked)
         return nullptr;
-    const unsigned long long want = lt_tuned(ta, tb, M, N, K, epi);
+    const bool listed = lt_tuned(ta, tb, M, N, K, epi);
     int pick = -1;
     for (int i = 0; i < n; ++i)
     {
@@ -329,9 +358,11 @@ LtPlan *lt_plan(int dev, bool ta, bool tb, int M, int N, int K, int lda, int ldb
             continue;
         if (pick < 0)
             pick = i;  // the heuristic's first workspace-free choice
-        if (want && fnv1a64(hipblaslt_ext::getKernelNameFromAlgo(g_lt[dev], res[i].algo)) == want)
+        if (listed &&
+            lt_tuned(ta, tb, M, N, K, epi, fnv1a64(hipblaslt_ext::getKernelNameFromAlgo(g_lt[dev], res[i].algo))))
         {
             pick = i;
+            q.tuned = true;
             break;
         }
     }
@@ -348,14 +379,15 @@ LtPlan *lt_plan(int dev, bool ta, bool tb, int M, int N, int K, int lda, int ldb
 // biased product to aux. Returns 1 when hipBLASLt has no plan (nothing was
 // enqueued), 0 on success, a GPT_HIP_OPS_E* code on failure.
 int lt_gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int K, float alpha, const float *A,
-            int lda, const float *B, int ldb, float beta, float *C, int ldc, int epi, const float *bias, float *aux)
+            int lda, const float *B, int ldb, float beta, float *C, int ldc, int epi, const float *bias, float *aux,
+            bool need_tuned = false)
 {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess)
         return fail(GPT_HIP_OPS_ENODEV, "%s: no current HIP device", op);
     std::lock_guard<std::mutex> lock(g_lt_mu);
     LtPlan *q = lt_plan(dev, ta, tb, M, N, K, lda, ldb, ldc, epi);
-    if (!q)
+    if (!q || (need_tuned && !q->tuned))
         return 1;
     if (epi >= 1 &&
         hipblasLtMatmulDescSetAttribute(q->desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)))
@@ -376,14 +408,16 @@ int lt_gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int 
 
 bool use_lt(bool ta, int N) { return ta || N <= 1024; }
 
-// Plain GEMM: hipBLASLt where use_lt says so or a tuned solution exists and
-// it has a plan, else rocBLAS.
+// Plain GEMM: hipBLASLt where use_lt says so and it has a plan, or where the
+// loaded hipBLASLt offers the table's kernel for the shape; else rocBLAS.
 int gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int K, float alpha, const float *A, int lda,
          const float *B, int ldb, float beta, float *C, int ldc)
 {
-    if (use_lt(ta, N) || lt_tuned(ta, tb, M, N, K, 0))
+    const bool lt = use_lt(ta, N);
+    if (lt || lt_tuned(ta, tb, M, N, K, 0))
     {
-        const int rc = lt_gemm(op, st, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, 0, nullptr, nullptr);
+        const int rc =
+            lt_gemm(op, st, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, 0, nullptr, nullptr, !lt);
         if (rc != 1)
             return rc;
     }
@@ -539,18 +573,19 @@ int gpt_hip_linear_activation_forward_f32(float *y, float *act, const float *x, 
         return rc;
     const hipStream_t st = as_stream(stream);
     const int M = (int)rows, K = input_size, N = output_size;
-    // y [M x N] = x [M x K] w [K x N] + b. On hipBLASLt (use_lt, or a tuned
-    // bias-epilogue solution) the bias goes in its epilogue, and with
-    // activation the GELU too when g_fused_gelu allows it and the shape has no
-    // tuned bias-only solution (D = act, pre-activation y as the auxiliary
-    // output), else one pass of this library's GELU over y. On rocBLAS one
-    // pass adds the bias and writes the GELU.
-    const bool tuned = lt_tuned(false, false, M, N, K, 1) != 0;
-    if (!use_lt(false, N) && !tuned)
+    // y [M x N] = x [M x K] w [K x N] + b. On hipBLASLt (use_lt, or the
+    // table's bias-epilogue kernel for a wide shape) the bias goes in its
+    // epilogue, and with activation the GELU too when g_fused_gelu allows it
+    // and the table lists no bias-only kernel for the shape (D = act,
+    // pre-activation y as the auxiliary output), else one pass of this
+    // library's GELU over y. On rocBLAS one pass adds the bias and writes the
+    // GELU.
+    const bool lt = use_lt(false, N), listed = lt_tuned(false, false, M, N, K, 1);
+    if (!lt && !listed)
     {
         // rocBLAS below
     }
-    else if (activation && g_fused_gelu && !tuned)
+    else if (activation && g_fused_gelu && !listed)
     {
         const int rc = lt_gemm(op, st, false, false, M, N, K, 1.f, x, K, w, N, 0.f, act, N, 2, b, y);
         if (rc != 1)
@@ -558,7 +593,7 @@ int gpt_hip_linear_activation_forward_f32(float *y, float *act, const float *x, 
     }
     else
     {
-        const int rc = lt_gemm(op, st, false, false, M, N, K, 1.f, x, K, w, N, 0.f, y, N, 1, b, nullptr);
+        const int rc = lt_gemm(op, st, false, false, M, N, K, 1.f, x, K, w, N, 0.f, y, N, 1, b, nullptr, !lt);
         if (rc == 0)
             return activation ? launched(op, gpt_ops::launch_gelu(act, y, rows, N, st)) : 0;
         if (rc != 1)
