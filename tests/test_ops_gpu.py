@@ -189,6 +189,40 @@ def test_linear_fwd_bwd(dev, B, T, n_in, n_out, activation):
     assert_close("GELU backward", host(ga), ga_r, RTOL)
 
 
+@pytest.mark.parametrize("n_in,n_out,activation", [(768, 2304, False), (768, 768, False), (768, 3072, True),
+                                                    (3072, 768, False)])
+def test_linear_at_gpt2_step_shapes(dev, n_in, n_out, activation):
+    """The GPT-2 124M layer shapes at B=16, T=256 (4096 rows), where the
+    library takes its table of tuned GEMM kernels: y = x w + b, GELU, grad_x,
+    grad_w (accumulated) and grad_b against float64 numpy (the oracle's C
+    loops would take minutes here; its GELU, gelu_tanh in ops_oracle.c, is
+    restated in float64)."""
+    import torch
+
+    B, T = 16, 256
+    r = rng(7 + n_in + n_out)
+    x, w = f32(r.standard_normal((B, T, n_in))), f32(r.standard_normal((n_in, n_out)) / np.sqrt(n_in))
+    b = f32(0.1 * r.standard_normal(n_out))
+    gy, gw0, gb0 = f32(r.standard_normal((B, T, n_out))), f32(r.standard_normal((n_in, n_out))), \
+        f32(r.standard_normal(n_out))
+    x64, w64, gy64 = (a.astype(np.float64).reshape(-1, a.shape[-1]) for a in (x, w, gy))
+    y_r = x64 @ w64 + b.astype(np.float64)
+    dx, dw, db, dgy = (to_dev(dev, a) for a in (x, w, b, gy))
+    y, act = torch.empty((B, T, n_out), device=dev), torch.empty((B, T, n_out), device=dev)
+    ops.device_linear_activation_fused_forward(y, act if activation else None, dx, dw, db, activation, B, T, n_in,
+                                               n_out)
+    assert_close("linear y", host(y).reshape(-1, n_out), y_r, RTOL)
+    if activation:
+        ys = host(y).astype(np.float64)
+        a_r = 0.5 * ys * (1.0 + np.tanh(0.79788456 * (ys + 0.044715 * ys ** 3)))
+        assert_close("linear GELU", host(act), a_r, RTOL)
+    gx, dgw, dgb = torch.empty((B, T, n_in), device=dev), to_dev(dev, gw0), to_dev(dev, gb0)
+    ops.device_linear_backward(gx, dgw, dgb, dgy, dx, dw, B, T, n_in, n_out)
+    assert_close("linear grad_x", host(gx).reshape(-1, n_in), gy64 @ w64.T, RTOL)
+    assert_close("linear grad_w", host(dgw), gw0.astype(np.float64) + x64.T @ gy64, RTOL)
+    assert_close("linear grad_b", host(dgb), gb0.astype(np.float64) + gy64.sum(0), RTOL)
+
+
 def test_gemm_ops_are_bitwise_repeatable(dev):
     """The GEMM ops (hipBLASLt / rocBLAS algorithms chosen once per shape)
     give the same bits on every call, accumulating outputs included."""
