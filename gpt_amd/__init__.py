@@ -12,6 +12,7 @@ from .attention import (  # noqa: F401
     attention_backward,
     attention_forward,
     device_flash_attention_backward,
+    device_flash_attention_backward_noalloc,
     device_flash_attention_forward,
     device_ok,
     lib_path,

@@ -55,6 +55,8 @@ def load_library():
         lib.gpt_hip_attn_fwd_f32.restype = i
         lib.gpt_hip_attn_bwd_f32.argtypes = [p, p, p, p, p, p, i, i, i, i, vp]
         lib.gpt_hip_attn_bwd_f32.restype = i
+        lib.gpt_hip_attn_bwd_f32_noalloc.argtypes = [p, p, p, p, p, p, i, i, i, i, vp]
+        lib.gpt_hip_attn_bwd_f32_noalloc.restype = i
         lib.gpt_hip_attn_last_error.argtypes = []
         lib.gpt_hip_attn_last_error.restype = ctypes.c_char_p
         lib.gpt_hip_attn_device_ok.argtypes = []
@@ -114,6 +116,19 @@ def device_flash_attention_backward(grad_x: Ptr, D_cache: Ptr, logsumexp: Ptr, g
                                     num_heads: int, stream=None) -> None:
     """Overwrites grad_x [B,T,3C] with dQ|dK|dV and writes D_cache [B,T,H]."""
     rc = load_library().gpt_hip_attn_bwd_f32(
+        _addr(grad_x, "grad_x"), _addr(D_cache, "D_cache"), _addr(logsumexp, "logsumexp"),
+        _addr(grad_y, "grad_y"), _addr(y, "y"), _addr(qkv, "qkv"),
+        batch_size, seq_len, hidden_size, num_heads, _stream(stream))
+    _check(rc)
+
+
+def device_flash_attention_backward_noalloc(grad_x: Ptr, D_cache: Ptr, logsumexp: Ptr, grad_y: Ptr, y: Ptr,
+                                            qkv: Ptr, batch_size: int, seq_len: int, hidden_size: int,
+                                            num_heads: int, stream=None) -> None:
+    """As device_flash_attention_backward, but the library allocates no device
+    memory: its dS tiles live in a fixed per-device scratch array (head_dim 64
+    up to T = 5760; longer rows raise). Calls overlapping on one device race."""
+    rc = load_library().gpt_hip_attn_bwd_f32_noalloc(
         _addr(grad_x, "grad_x"), _addr(D_cache, "D_cache"), _addr(logsumexp, "logsumexp"),
         _addr(grad_y, "grad_y"), _addr(y, "y"), _addr(qkv, "qkv"),
         batch_size, seq_len, hidden_size, num_heads, _stream(stream))

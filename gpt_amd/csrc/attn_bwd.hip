@@ -807,13 +807,19 @@ hipError_t launch_bwd_prep(float *grad_x, float *D, const float *dy, const float
     return hipGetLastError();
 }
 
-size_t bwd_d64_workspace_bytes(const Shape &s, int *bh_per_chunk)
+size_t bwd_d64_workspace_bytes(const Shape &s, size_t cap, int *bh_per_chunk)
 {
     const long n_qb = (s.T + 31) / 32;
     const size_t per_bh = (size_t)(n_qb * (n_qb + 1) / 2) * 4096;
     const long BH = (long)s.B * s.H;
-    long chunk = (long)(kWorkspaceCap / per_bh);
-    chunk = chunk < 1 ? 1 : (chunk > BH ? BH : chunk);
+    if (per_bh > cap)
+    {
+        if (bh_per_chunk)
+            *bh_per_chunk = 0;
+        return per_bh;
+    }
+    long chunk = (long)(cap / per_bh);
+    chunk = chunk > BH ? BH : chunk;
     if (bh_per_chunk)
         *bh_per_chunk = (int)chunk;
     return per_bh * (size_t)chunk;

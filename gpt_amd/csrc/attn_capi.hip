@@ -15,6 +15,9 @@
 #include <stdint.h>
 #include <stdio.h>
 
+// 64 MiB (kScratchBytes): dS tiles of one (b, h) up to T = 5760.
+static __device__ __align__(256) float scratch[(size_t(64) << 20) / sizeof(float)];
+
 namespace {
 
 thread_local char g_err[512] = "";
@@ -153,6 +156,46 @@ hipError_t workspace_get(void **out, size_t bytes, hipStream_t st)
     return hipSuccess;
 }
 
+// Scratch of the no-allocation backward (gpt_hip_attn_bwd_f32_noalloc): a
+// fixed device array that holds the dS tiles in place of the per-stream
+// workspace. Each device the library runs on has its own copy, allocated when
+// the code object is loaded there and held until the process ends. Host code
+// never uses the array's name as an address: the device address of this
+// device's copy is looked up once per device (hipGetSymbolAddress) and kept
+// in g_scratch.
+constexpr size_t kScratchBytes = sizeof(scratch);
+
+constexpr int kMaxDevices = 64;
+struct ScratchAddr
+{
+    std::once_flag once;
+    hipError_t err = hipSuccess;
+    float *p = nullptr;
+};
+ScratchAddr g_scratch[kMaxDevices];
+
+// Device address of the current device's scratch array (looked up on the
+// first call per device, with that device current).
+hipError_t scratch_addr(float **out)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return e;
+    if (dev < 0 || dev >= kMaxDevices)
+        return hipErrorInvalidDevice;
+    ScratchAddr &s = g_scratch[dev];
+    std::call_once(s.once, [&s]() {
+        void *p = nullptr;
+        s.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        s.p = s.err == hipSuccess ? static_cast<float *>(p) : nullptr;
+    });
+    if (s.err != hipSuccess)
+        return s.err;
+    *out = s.p;
+    return hipSuccess;
+}
+
 }  // namespace
 
 namespace gpt_attn {
@@ -191,6 +234,76 @@ bool timer_slot(int kind, hipEvent_t *e0, hipEvent_t *e1)
 
 }  // namespace gpt_attn
 
+namespace {
+
+// Body of both backward entry points. The default one takes its dS workspace
+// from the per-(device, stream) buffers above; the no-allocation one
+// (noalloc) uses the device's scratch array, allocates nothing and refuses a
+// call in which one (b, h)'s dS tiles exceed it.
+int backward(const char *op, bool noalloc, float *grad_x, float *D_cache, const float *lse, const float *grad_y,
+             const float *y, const float *qkv, int batch_size, int seq_len, int hidden_size, int num_heads,
+             void *stream)
+{
+    gpt_attn::Shape s;
+    if (int rc = check_shape(op, batch_size, seq_len, hidden_size, num_heads, &s))
+        return rc;
+    if (batch_size == 0 || seq_len == 0)
+        return 0;
+    if (!grad_x || !D_cache || !lse || !grad_y || !y || !qkv)
+        return fail(GPT_HIP_ATTN_ENULL, "%s: NULL tensor pointer", op);
+    if (int rc = check_device(op))
+        return rc;
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int path = g_path;
+    const bool mfma = path != 1 && s.d == 64 && slice_fits_buffer(s) && ds_fits_buffer(s) &&
+                      aligned16(grad_x) && aligned16(grad_y) && aligned16(y) && aligned16(qkv);
+    if (!mfma)
+    {
+        const hipError_t e = gpt_attn::launch_bwd_general(grad_x, D_cache, lse, grad_y, y, qkv, s, st);
+        if (e != hipSuccess)
+            return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
+        return 0;
+    }
+    if (path == 2 && !noalloc)
+    {
+        const hipError_t e = gpt_attn::launch_bwd_d64_atomic(grad_x, D_cache, lse, grad_y, y, qkv, s, st);
+        if (e != hipSuccess)
+            return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
+        return 0;
+    }
+    int chunk = 0;
+    const size_t bytes =
+        gpt_attn::bwd_d64_workspace_bytes(s, noalloc ? kScratchBytes : gpt_attn::kWorkspaceCap, &chunk);
+    void *ws = nullptr;
+    hipError_t e = hipSuccess;
+    if (noalloc)
+    {
+        if (chunk == 0)
+            return fail(GPT_HIP_ATTN_ERANGE,
+                        "%s: one (b, h) needs %zu bytes of dS scratch at T=%d, more than the %zu-byte scratch "
+                        "array (T <= 5760 fits)",
+                        op, bytes, s.T, kScratchBytes);
+        float *p = nullptr;
+        e = scratch_addr(&p);
+        if (e != hipSuccess)
+            return fail(GPT_HIP_ATTN_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", op,
+                        hipGetErrorString(e));
+        ws = p;
+    }
+    else
+    {
+        e = workspace_get(&ws, bytes, st);
+        if (e != hipSuccess)
+            return fail(GPT_HIP_ATTN_ENOMEM, "%s: workspace of %zu bytes: %s", op, bytes, hipGetErrorString(e));
+    }
+    e = gpt_attn::launch_bwd_d64(grad_x, D_cache, lse, grad_y, y, qkv, static_cast<float *>(ws), chunk, s, st);
+    if (e != hipSuccess)
+        return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
+    return 0;
+}
+
+}  // namespace
+
 extern "C" {
 
 int gpt_hip_attn_fwd_f32(float *y, float *lse, const float *qkv, int batch_size, int seq_len,
@@ -219,43 +332,16 @@ int gpt_hip_attn_bwd_f32(float *grad_x, float *D_cache, const float *lse, const 
                          const float *y, const float *qkv, int batch_size, int seq_len, int hidden_size,
                          int num_heads, void *stream)
 {
-    static const char *op = "gpt_hip_attn_bwd_f32";
-    gpt_attn::Shape s;
-    if (int rc = check_shape(op, batch_size, seq_len, hidden_size, num_heads, &s))
-        return rc;
-    if (batch_size == 0 || seq_len == 0)
-        return 0;
-    if (!grad_x || !D_cache || !lse || !grad_y || !y || !qkv)
-        return fail(GPT_HIP_ATTN_ENULL, "%s: NULL tensor pointer", op);
-    if (int rc = check_device(op))
-        return rc;
-    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const bool mfma = g_path != 1 && s.d == 64 && slice_fits_buffer(s) && ds_fits_buffer(s) &&
-                      aligned16(grad_x) && aligned16(grad_y) && aligned16(y) && aligned16(qkv);
-    if (!mfma)
-    {
-        const hipError_t e = gpt_attn::launch_bwd_general(grad_x, D_cache, lse, grad_y, y, qkv, s, st);
-        if (e != hipSuccess)
-            return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
-        return 0;
-    }
-    if (g_path == 2)
-    {
-        const hipError_t e = gpt_attn::launch_bwd_d64_atomic(grad_x, D_cache, lse, grad_y, y, qkv, s, st);
-        if (e != hipSuccess)
-            return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
-        return 0;
-    }
-    int chunk = 0;
-    const size_t bytes = gpt_attn::bwd_d64_workspace_bytes(s, &chunk);
-    void *ws = nullptr;
-    hipError_t e = workspace_get(&ws, bytes, st);
-    if (e != hipSuccess)
-        return fail(GPT_HIP_ATTN_ENOMEM, "%s: workspace of %zu bytes: %s", op, bytes, hipGetErrorString(e));
-    e = gpt_attn::launch_bwd_d64(grad_x, D_cache, lse, grad_y, y, qkv, static_cast<float *>(ws), chunk, s, st);
-    if (e != hipSuccess)
-        return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
-    return 0;
+    return backward("gpt_hip_attn_bwd_f32", false, grad_x, D_cache, lse, grad_y, y, qkv, batch_size, seq_len,
+                    hidden_size, num_heads, stream);
+}
+
+int gpt_hip_attn_bwd_f32_noalloc(float *grad_x, float *D_cache, const float *lse, const float *grad_y,
+                                 const float *y, const float *qkv, int batch_size, int seq_len,
+                                 int hidden_size, int num_heads, void *stream)
+{
+    return backward("gpt_hip_attn_bwd_f32_noalloc", true, grad_x, D_cache, lse, grad_y, y, qkv, batch_size,
+                    seq_len, hidden_size, num_heads, stream);
 }
 
 const char *gpt_hip_attn_last_error(void) { return g_err; }

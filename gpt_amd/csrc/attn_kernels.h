@@ -61,9 +61,11 @@ hipError_t launch_fwd_general(float *y, float *lse, const float *qkv, const Shap
 hipError_t launch_bwd_prep(float *grad_x, float *D, const float *dy, const float *y, const Shape &s,
                            hipStream_t st, int zero_dq);
 
-// Bytes of dS workspace launch_bwd_d64 needs, and the number of (b, h) pairs
-// processed per chunk with it.
-size_t bwd_d64_workspace_bytes(const Shape &s, int *bh_per_chunk);
+// Bytes of dS workspace launch_bwd_d64 needs when it may use at most `cap`
+// bytes, and the number of (b, h) pairs processed per chunk with it (0 when
+// one (b, h)'s dS tiles alone exceed `cap`; the return value is then that
+// one (b, h)'s size).
+size_t bwd_d64_workspace_bytes(const Shape &s, size_t cap, int *bh_per_chunk);
 
 // Backward, head_dim 64, fp32 MFMA, deterministic (D rows, dK/dV + dS tiles,
 // dQ from the dS tiles). `ws` holds bwd_d64_workspace_bytes(s) bytes.

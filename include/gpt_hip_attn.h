@@ -73,6 +73,28 @@ int gpt_hip_attn_bwd_f32(float *grad_x, float *D_cache, const float *lse,
                          int batch_size, int seq_len, int hidden_size, int num_heads,
                          void *stream);
 
+/* Causal attention backward that allocates nothing: the same arguments,
+ * results (bit for bit) and status codes as gpt_hip_attn_bwd_f32, but the
+ * head_dim-64 path keeps its dS tiles in a fixed 64 MiB device array of the
+ * library (one copy per device, allocated when the library's code object is
+ * loaded on that device and held until the process ends) instead of the
+ * per-stream workspace, and no call makes a hipMalloc / hipFree. Returns
+ * GPT_HIP_ATTN_ERANGE, before launching anything, when one (b, h)'s dS tiles
+ * exceed the array (head_dim 64 and T > 5760). Calls that take the general-d
+ * kernels (other head sizes, misaligned pointers) use no dS tiles and run as
+ * in gpt_hip_attn_bwd_f32; path 2 of gpt_hip_attn_set_path does not apply
+ * here (this entry point always takes the deterministic kernels). All calls on one
+ * device share the array: calls that overlap in time on one device (another
+ * stream, another host thread) race and must not be issued; calls ordered on
+ * one stream are safe. The array's contents are left from the last call.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). */
+int gpt_hip_attn_bwd_f32_noalloc(float *grad_x, float *D_cache, const float *lse,
+                                 const float *grad_y, const float *y, const float *qkv,
+                                 int batch_size, int seq_len, int hidden_size, int num_heads,
+                                 void *stream);
+
 /* Message for the last non-zero return on the calling thread ("" if none).
  * No reference counterpart: the reference prints and aborts instead
  * (src/backend/cuda/utils/cuda_utils.cuh:21-34); adapters that keep that
