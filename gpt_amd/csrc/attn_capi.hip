@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 #include <stdarg.h>
 #include <stdint.h>
@@ -21,7 +22,9 @@ static __device__ __align__(256) float scratch[(size_t(64) << 20) / sizeof(float
 namespace {
 
 thread_local char g_err[512] = "";
-int g_path = 0;  // 0 automatic, 1 general-d kernels only, 2 atomic-dQ backward
+// kernel selection (gpt_hip_attn_set_path): 0 automatic, 1 general-d kernels
+// only, 2 atomic-dQ backward; read once per call
+std::atomic<int> g_path{0};
 
 
 int fail(int code, const char *fmt, ...)
@@ -254,7 +257,7 @@ int backward(const char *op, bool noalloc, float *grad_x, float *D_cache, const 
     if (int rc = check_device(op))
         return rc;
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const int path = g_path;
+    const int path = g_path.load(std::memory_order_relaxed);
     const bool mfma = path != 1 && s.d == 64 && slice_fits_buffer(s) && ds_fits_buffer(s) &&
                       aligned16(grad_x) && aligned16(grad_y) && aligned16(y) && aligned16(qkv);
     if (!mfma)
@@ -320,7 +323,8 @@ int gpt_hip_attn_fwd_f32(float *y, float *lse, const float *qkv, int batch_size,
     if (int rc = check_device(op))
         return rc;
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const bool mfma = g_path != 1 && s.d == 64 && slice_fits_buffer(s) && aligned16(y) && aligned16(qkv);
+    const bool mfma = g_path.load(std::memory_order_relaxed) != 1 && s.d == 64 && slice_fits_buffer(s) &&
+                      aligned16(y) && aligned16(qkv);
     const hipError_t e = mfma ? gpt_attn::launch_fwd_d64(y, lse, qkv, s, st)
                               : gpt_attn::launch_fwd_general(y, lse, qkv, s, st);
     if (e != hipSuccess)
@@ -404,9 +408,7 @@ int gpt_hip_attn_set_path(int path)
 {
     if (path < 0 || path > 2)
         return fail(GPT_HIP_ATTN_EINVAL, "gpt_hip_attn_set_path: unknown path %d", path);
-    const int prev = g_path;
-    g_path = path;
-    return prev;
+    return g_path.exchange(path);
 }
 
 }  // extern "C"
