@@ -11,10 +11,12 @@ value = algorithmic FLOPs / GPU time, FLOPs = 12 * 7 * B * H * d * T * (T+1)
 including the diagonal; exp and masking not counted).
 
 Also reported:
-  kernels       per-kernel average durations over a second pass of the same
-                steps, from the library's launch timer (gpt_hip_attn_timing_*:
-                each head_dim-64 kernel launched by hipExtLaunchKernelGGL with
-                an event pair that the dispatch's own start and end set)
+  kernels       per-kernel average durations and algorithmic TFLOP/s over a
+                second pass of the same steps, from the library's launch timer
+                (gpt_hip_attn_timing_*: each head_dim-64 kernel launched by
+                hipExtLaunchKernelGGL with an event pair that the dispatch's
+                own start and end set); kernel_ms_per_step = their sum per
+                step (the rest of ms_per_step is the gaps between kernels)
   roofline      the dominant kernel (most GPU time): algorithmic FLOPs per
                 launch / its average launch duration, against 157.3 TFLOP/s;
                 `traffic` = its measured HBM bytes per launch, read from
@@ -66,11 +68,12 @@ def attn_flops(b, t, h, d, fwd=True, bwd=True):
 
 # Algorithmic FLOPs of one launch of each head_dim-64 kernel, in units of
 # B*H*d*T(T+1) (= 2 FLOPs x d per causal pair): forward QK^T + PV = 2;
-# dK/dV kernel S + dP + dV + dK = 4; dQ kernel dS K = 1. The D-row kernel does
-# no matrix work (bandwidth-bound: reads dO and O).
-KERNEL_FLOP_UNITS = {"fwd": 2, "bwd_dkdv": 4, "bwd_dq": 1, "bwd_rowdot": 0}
+# two-launch backward: dK/dV kernel S + dP + dV + dK = 4, dQ kernel dS K = 1;
+# fused backward (T <= 256, one launch) all five = 5. The D-row kernel does no
+# matrix work (bandwidth-bound: reads dO and O).
+KERNEL_FLOP_UNITS = {"fwd": 2, "bwd_dkdv": 4, "bwd_dq": 1, "bwd_fused": 5, "bwd_rowdot": 0}
 KERNEL_SYMBOL = {"fwd": "fwd_qs_d64_kernel", "bwd_dkdv": "bwd_dkdv_d64_kernel", "bwd_dq": "bwd_dq_d64_kernel",
-                 "bwd_rowdot": "bwd_rowdot_d64_kernel"}
+                 "bwd_fused": "bwd_fused_d64_kernel", "bwd_rowdot": "bwd_rowdot_d64_kernel"}
 COPY_BYTES = 256 << 20
 
 
@@ -134,9 +137,9 @@ def parse():
                     help="time BASELINE config 5(b) (forward, B=1, T=1..256) instead of the headline")
     ap.add_argument("--ops", action="store_true",
                     help="time the GPT-2 ops around attention (libgpt_hip_ops.so) instead of the headline")
-    ap.add_argument("--bwd-path", type=int, default=0, choices=(0, 2),
-                    help="backward variant for profiling: 0 deterministic dS-tile dQ (default), "
-                         "2 fp32-atomic dQ (gpt_hip_attn_set_path)")
+    ap.add_argument("--bwd-path", type=int, default=0, choices=(0, 2, 3),
+                    help="backward variant for profiling (gpt_hip_attn_set_path): 0 default (one fused "
+                         "launch at T <= 256), 2 fp32-atomic dQ, 3 two-launch (dK/dV + dS tiles, then dQ)")
     return ap.parse_args()
 
 
@@ -523,20 +526,12 @@ def main():
         Dc.append(torch.empty(B, T, H, device=dev))
     torch.cuda.synchronize()
 
-    def step(ev=None):
+    def step():
         for layer in range(LAYERS):
-            if ev is not None:
-                ev[0][layer].record(stream)
             gpt_amd.device_flash_attention_forward(y[layer], lse[layer], qkv[layer], B, T, C, H, stream)
-            if ev is not None:
-                ev[1][layer].record(stream)
         for layer in reversed(range(LAYERS)):
-            if ev is not None:
-                ev[2][layer].record(stream)
             gpt_amd.device_flash_attention_backward(gx[layer], Dc[layer], lse[layer], dout[layer], y[layer],
                                                     qkv[layer], B, T, C, H, stream)
-            if ev is not None:
-                ev[3][layer].record(stream)
 
     for _ in range(args.warmup):
         step()
@@ -553,35 +548,24 @@ def main():
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
 
-    # Breakdown pass: the same K steps again with an event pair around every op
-    # (torch events) and the dispatch timestamps of every kernel launch (the
-    # library's launch timer).
-    # Kept out of the timed region because the extra event packets between
-    # back-to-back kernels slow the step down by ~10%.
-    mk = lambda: [torch.cuda.Event(enable_timing=True) for _ in range(LAYERS)]  # noqa: E731
-    evs = [[mk() for _ in range(4)] for _ in range(args.steps)]
+    # Breakdown pass: the same K steps again with the library's launch timer
+    # (each kernel's own dispatch start and end timestamps). Kept out of the
+    # timed region, whose step time alone is the metric.
     gpt_amd.timing_enable(True)
     torch.cuda.synchronize()
     for k in range(args.steps):
-        step(evs[k])
+        step()
     torch.cuda.synchronize()
     per_kernel = gpt_amd.timing_read()
     gpt_amd.timing_enable(False)
-    fwd_ms = [e[0][i].elapsed_time(e[1][i]) for e in evs for i in range(LAYERS)]
-    bwd_ms = [e[2][i].elapsed_time(e[3][i]) for e in evs for i in range(LAYERS)]
 
     ms_per_step = total_ms / args.steps
     step_flops = LAYERS * attn_flops(B, T, H, D_HEAD)
     tflops = step_flops / (ms_per_step * 1e-3) / 1e12
-    bwd_avg_ms = float(np.mean(bwd_ms))
-    fwd_avg_ms = float(np.mean(fwd_ms))
-    bwd_flops = attn_flops(B, T, H, D_HEAD, fwd=False)
-    fwd_flops = attn_flops(B, T, H, D_HEAD, bwd=False)
-    bwd_tf = bwd_flops / (bwd_avg_ms * 1e-3) / 1e12
-    fwd_tf = fwd_flops / (fwd_avg_ms * 1e-3) / 1e12
 
-    kernels = {k: {"avg_us": round(1e3 * ms / n, 3), "launches": n}
-               for k, (ms, n) in per_kernel.items() if n > 0}
+    kernels = {k: {"avg_us": round(1e3 * ms / n, 3), "launches": n, "tflops": round(
+                   KERNEL_FLOP_UNITS[k] * B * H * D_HEAD * T * (T + 1) / (ms / n * 1e-3) / 1e12, 3)}
+               for k, (ms, n) in per_kernel.items() if n > 0 and k in KERNEL_FLOP_UNITS}
     dom = max((k for k in kernels if k in KERNEL_FLOP_UNITS), key=lambda k: per_kernel[k][0])
     dom_ms = per_kernel[dom][0] / per_kernel[dom][1]
     dom_flops = KERNEL_FLOP_UNITS[dom] * B * H * D_HEAD * T * (T + 1)
@@ -613,9 +597,8 @@ def main():
             **({"bwd_path": args.bwd_path} if args.bwd_path else {}),
         },
         "pct_fp32_mfma_peak": round(100 * tflops / PEAK_FP32_MFMA_TFLOPS, 2),
-        "fwd": {"avg_ms": round(fwd_avg_ms, 5), "tflops": round(fwd_tf, 3)},
-        "bwd": {"avg_ms": round(bwd_avg_ms, 5), "tflops": round(bwd_tf, 3)},
         "kernels": kernels,
+        "kernel_ms_per_step": round(sum(ms for ms, n in per_kernel.values()) / args.steps, 4),
         "roofline": {
             "kernel": KERNEL_SYMBOL[dom],
             "bound": "mfma",

@@ -163,7 +163,7 @@ def device_ok() -> bool:
     return bool(load_library().gpt_hip_attn_device_ok())
 
 
-KERNEL_KINDS = ("fwd", "bwd_rowdot", "bwd_dkdv", "bwd_dq", "other")
+KERNEL_KINDS = ("fwd", "bwd_rowdot", "bwd_dkdv", "bwd_dq", "other", "bwd_fused")
 
 
 def timing_enable(on: bool = True) -> None:
@@ -184,8 +184,10 @@ def timing_read() -> dict:
 
 
 def set_path(path: int) -> int:
-    """0 = automatic (MFMA kernels for head_dim 64, deterministic backward),
-    1 = general-d kernels only, 2 = as 0 but with the fp32-atomic dQ backward.
+    """0 = automatic (MFMA kernels for head_dim 64, deterministic backward:
+    one fused launch for T <= 256, dK/dV then dQ beyond), 1 = general-d
+    kernels only, 2 = as 0 but with the fp32-atomic dQ backward, 3 = as 0 but
+    the two-launch backward at every T.
     Returns the previous setting. Test and tuning hook; process-wide."""
     rc = load_library().gpt_hip_attn_set_path(path)
     if rc < 0:

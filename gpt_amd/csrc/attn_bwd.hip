@@ -825,8 +825,15 @@ size_t bwd_d64_workspace_bytes(const Shape &s, size_t cap, int *bh_per_chunk)
     return per_bh * (size_t)chunk;
 }
 
-// Compute units of the current device (cached per device; 0 if unknown).
-static int cu_count()
+hipError_t launch_bwd_rowdot_d64(float *D, const float *dy, const float *y, const Shape &s, hipStream_t st)
+{
+    const long n4 = (long)s.B * s.T * 16L * s.H;
+    launch_timed(kKindRowdot, bwd_rowdot_d64_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), st, D, dy, y,
+                 n4);
+    return hipGetLastError();
+}
+
+int device_cu_count()
 {
     static int cached[64] = {0};
     int dev = 0;
@@ -854,10 +861,7 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
     hipError_t e = hipSuccess;
     if (!fuse_d)
     {
-        const long n4 = (long)s.B * s.T * 16L * s.H;
-        launch_timed(kKindRowdot, bwd_rowdot_d64_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), st, D, dy, y,
-                     n4);
-        e = hipGetLastError();
+        e = launch_bwd_rowdot_d64(D, dy, y, s, st);
         if (e != hipSuccess)
             return e;
     }
@@ -870,10 +874,10 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
         const dim3 g((unsigned)((long)((s.T + 63) / 64) * cnt));
         if (fuse_d)
             launch_timed(kKindDkdv, bwd_dkdv_d64_kernel<true>, g, dim3(256), st, grad_x, ws, lse, D, dy, y, qkv, s.T,
-                         s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale, cu_count());
+                         s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale, device_cu_count());
         else
             launch_timed(kKindDkdv, bwd_dkdv_d64_kernel<false>, g, dim3(256), st, grad_x, ws, lse, D, dy, y, qkv,
-                         s.T, s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale, cu_count());
+                         s.T, s.C, s.H, bh0, cnt, n_qb, scale * kLog2e, scale, device_cu_count());
         const unsigned dq_blocks = (unsigned)((long)((n_qb + 1) / 2) * cnt);  // one workgroup per pair
         launch_timed(kKindDq, bwd_dq_d64_kernel, dim3(dq_blocks), dim3(256), st, grad_x, ws, qkv, s.T, s.C, s.H,
                      bh0, cnt, n_qb, scale);

@@ -16,14 +16,16 @@
 #include <stdint.h>
 #include <stdio.h>
 
-// 64 MiB (kScratchBytes): dS tiles of one (b, h) up to T = 5760.
-static __device__ __align__(256) float scratch[(size_t(64) << 20) / sizeof(float)];
+// 65 MiB: the backward's control block (1 MiB) and 64 MiB of dS tiles (one
+// (b, h)'s tiles fit up to T = 5760).
+static __device__ __align__(256) float scratch[(size_t(65) << 20) / sizeof(float)];
 
 namespace {
 
 thread_local char g_err[512] = "";
 // kernel selection (gpt_hip_attn_set_path): 0 automatic, 1 general-d kernels
-// only, 2 atomic-dQ backward; read once per call
+// only, 2 atomic-dQ backward, 3 two-launch backward at every T; read once per
+// call
 std::atomic<int> g_path{0};
 
 
@@ -148,8 +150,12 @@ hipError_t workspace_get(void **out, size_t bytes, hipStream_t st)
             w->bytes = 0;
         }
         e = hipMalloc(&w->p, bytes);
+        if (e == hipSuccess)  // the fused backward's control block starts out zeroed
+            e = hipMemsetAsync(w->p, 0, gpt_attn::kCtlBytes, st);
         if (e != hipSuccess)
         {
+            if (w->p)
+                (void)hipFree(w->p);
             w->p = nullptr;
             return e;
         }
@@ -166,7 +172,7 @@ hipError_t workspace_get(void **out, size_t bytes, hipStream_t st)
 // never uses the array's name as an address: the device address of this
 // device's copy is looked up once per device (hipGetSymbolAddress) and kept
 // in g_scratch.
-constexpr size_t kScratchBytes = sizeof(scratch);
+constexpr size_t kScratchBytes = sizeof(scratch) - gpt_attn::kCtlBytes;  // for dS tiles
 
 constexpr int kMaxDevices = 64;
 struct ScratchAddr
@@ -277,6 +283,11 @@ int backward(const char *op, bool noalloc, float *grad_x, float *D_cache, const 
     int chunk = 0;
     const size_t bytes =
         gpt_attn::bwd_d64_workspace_bytes(s, noalloc ? kScratchBytes : gpt_attn::kWorkspaceCap, &chunk);
+    // the fused backward's control block holds one counter per (b, h, query
+    // block) of a chunk
+    const long n_qb = (s.T + 31) / 32;
+    if (chunk > 0 && (long)gpt_attn::bwd_fused_ctl_ints(s, chunk) * 4 > (long)gpt_attn::kCtlBytes)
+        chunk = (int)((gpt_attn::kCtlBytes / 4 - 32) / n_qb);
     void *ws = nullptr;
     hipError_t e = hipSuccess;
     if (noalloc)
@@ -295,11 +306,21 @@ int backward(const char *op, bool noalloc, float *grad_x, float *D_cache, const 
     }
     else
     {
-        e = workspace_get(&ws, bytes, st);
+        e = workspace_get(&ws, gpt_attn::kCtlBytes + bytes, st);
         if (e != hipSuccess)
-            return fail(GPT_HIP_ATTN_ENOMEM, "%s: workspace of %zu bytes: %s", op, bytes, hipGetErrorString(e));
+            return fail(GPT_HIP_ATTN_ENOMEM, "%s: workspace of %zu bytes: %s", op, gpt_attn::kCtlBytes + bytes,
+                        hipGetErrorString(e));
     }
-    e = gpt_attn::launch_bwd_d64(grad_x, D_cache, lse, grad_y, y, qkv, static_cast<float *>(ws), chunk, s, st);
+    // workspace layout: [control block | dS tiles]
+    int *ctl = static_cast<int *>(ws);
+    float *dsw = reinterpret_cast<float *>(static_cast<char *>(ws) + gpt_attn::kCtlBytes);
+    // the fused kernel where its grid is resident at once (T <= 256), unless
+    // path 3 asks for the two-launch split
+    const int n_cu = gpt_attn::device_cu_count();
+    if (path != 3 && gpt_attn::bwd_fused_d64_fits(s, chunk, n_cu))
+        e = gpt_attn::launch_bwd_fused_d64(grad_x, D_cache, lse, grad_y, y, qkv, dsw, ctl, n_cu, s, st);
+    else
+        e = gpt_attn::launch_bwd_d64(grad_x, D_cache, lse, grad_y, y, qkv, dsw, chunk, s, st);
     if (e != hipSuccess)
         return fail(GPT_HIP_ATTN_ELAUNCH, "%s: launch failed: %s", op, hipGetErrorString(e));
     return 0;
@@ -406,7 +427,7 @@ int gpt_hip_attn_device_ok(void)
 
 int gpt_hip_attn_set_path(int path)
 {
-    if (path < 0 || path > 2)
+    if (path < 0 || path > 3)
         return fail(GPT_HIP_ATTN_EINVAL, "gpt_hip_attn_set_path: unknown path %d", path);
     return g_path.exchange(path);
 }

@@ -21,7 +21,8 @@ enum KernelKind
     kKindDkdv = 2,      // bwd_dkdv_d64_kernel
     kKindDq = 3,        // bwd_dq_d64_kernel
     kKindOther = 4,     // general-d kernels, atomic-variant kernels
-    kNumKinds = 5
+    kKindFused = 5,     // bwd_fused_d64_kernel (dK/dV + dS tiles + dQ, one launch)
+    kNumKinds = 6
 };
 
 // Brackets the launches between begin and end with HIP events on `st` when the
@@ -71,6 +72,29 @@ size_t bwd_d64_workspace_bytes(const Shape &s, size_t cap, int *bh_per_chunk);
 // dQ from the dS tiles). `ws` holds bwd_d64_workspace_bytes(s) bytes.
 hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
                           const float *qkv, float *ws, int bh_per_chunk, const Shape &s, hipStream_t st);
+
+// Control block of the persistent fused backward: 32 queue ints plus one
+// completion counter per (b, h, query block) of a chunk. It sits at the start
+// of the workspace, is zeroed when the workspace is allocated and is left
+// all zeros by every launch.
+constexpr size_t kCtlBytes = size_t(1) << 20;
+size_t bwd_fused_ctl_ints(const Shape &s, int bh_per_chunk);
+
+// Backward, head_dim 64, fp32 MFMA, deterministic, one launch (plus the D-row
+// kernel for T > 256): one dK/dV item per workgroup, then dQ items that start
+// on each query block as soon as its dS tiles are complete. Only for calls
+// whose whole grid is resident at once and needs one chunk
+// (bwd_fused_d64_fits). `ws` holds the dS tiles of all B * H (b, h), `ctl`
+// the control block (all zeros on entry and on exit); n_cu = compute units.
+bool bwd_fused_d64_fits(const Shape &s, int bh_per_chunk, int n_cu);
+hipError_t launch_bwd_fused_d64(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
+                                const float *qkv, float *ws, int *ctl, int n_cu, const Shape &s, hipStream_t st);
+
+// D = rowsum(dO * O) for head_dim 64 (bwd_rowdot_d64_kernel).
+hipError_t launch_bwd_rowdot_d64(float *D, const float *dy, const float *y, const Shape &s, hipStream_t st);
+
+// Compute units of the current device (cached per device; 0 if unknown).
+int device_cu_count();
 
 // Backward, head_dim 64, fp32 MFMA with fp32-atomic dQ accumulation (D rows +
 // dQ zeroing, then the fused dK/dV/dQ kernel).

@@ -19,7 +19,8 @@
  *   - Softmax scale is 1/sqrt(d); the causal mask keeps key j <= query i.
  *   - `stream` is a hipStream_t passed as void*; NULL means the default stream.
  *     Work is enqueued asynchronously. The forward allocates nothing. The
- *     head_dim-64 backward uses a dS workspace (4 KiB per 32x32 causal tile,
+ *     head_dim-64 backward uses a workspace (a 1 MiB control block, all
+ *     zeros between calls, then the dS tiles: 4 KiB per 32x32 causal tile,
  *     28 MiB at B=16 T=256 H=12, at most 2 GiB per call: larger problems run
  *     in (b, h) chunks) that the library allocates on first use, one buffer
  *     per (device, stream), grows when a call needs more (after waiting for
@@ -75,7 +76,8 @@ int gpt_hip_attn_bwd_f32(float *grad_x, float *D_cache, const float *lse,
 
 /* Causal attention backward that allocates nothing: the same arguments,
  * results (bit for bit) and status codes as gpt_hip_attn_bwd_f32, but the
- * head_dim-64 path keeps its dS tiles in a fixed 64 MiB device array of the
+ * head_dim-64 path keeps its dS tiles (64 MiB) and control block (1 MiB) in a
+ * fixed 65 MiB device array of the
  * library (one copy per device, allocated when the library's code object is
  * loaded on that device and held until the process ends) instead of the
  * per-stream workspace, and no call makes a hipMalloc / hipFree. Returns
@@ -114,9 +116,10 @@ int gpt_hip_attn_device_ok(void);
  * milliseconds and the launch count per kernel kind into ms[k] / count[k] for
  * k < n_kinds, forgets the recorded launches and returns how many there were.
  * Kinds: 0 head_dim-64 forward, 1 backward D rows (T > 256; up to T = 256
- * the dK/dV kernel computes them), 2 backward dK/dV (+ dS
- * tiles), 3 backward dQ, 4 everything else (general-d kernels, the atomic
- * variant). Not thread-safe. No reference counterpart (the reference times
+ * the backward kernels compute them), 2 backward dK/dV (+ dS tiles) of the
+ * two-launch form, 3 its dQ kernel, 4 everything else (general-d kernels, the
+ * atomic variant), 5 the fused one-launch backward (T <= 256). Not
+ * thread-safe. No reference counterpart (the reference times
  * whole training steps with a host clock, src/core/benchmark.h:5-16). */
 int gpt_hip_attn_timing_enable(int on);
 int gpt_hip_attn_timing_read(double *ms, int *count, int n_kinds);
@@ -131,6 +134,10 @@ int gpt_hip_attn_timing_read(double *ms, int *count, int n_kinds);
  *   path 2  as 0, but the head_dim-64 backward accumulates dQ with fp32
  *           global atomics (no workspace, not bitwise reproducible); kept to
  *           measure that design against the default
+ *   path 3  as 0, but the head_dim-64 backward always takes the two-launch
+ *           form (dK/dV + dS tiles, then dQ) instead of the single fused
+ *           launch that path 0 takes for T <= 256; kept to measure the two
+ *           against each other (both deterministic)
  * Returns the previous path, or GPT_HIP_ATTN_EINVAL for an unknown path.
  * No reference counterpart. */
 int gpt_hip_attn_set_path(int path);

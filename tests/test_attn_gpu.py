@@ -182,6 +182,70 @@ def test_atomic_dq_path_parity(dev, B, T):
         gpt_amd.set_path(prev)
 
 
+@pytest.mark.parametrize("B,T,C,H", [(16, 256, 768, 12), (3, 255, 768, 12), (5, 257, 768, 12), (1, 1, 64, 1),
+                                     (2, 64, 128, 2), (7, 129, 192, 3), (1, 33, 768, 12)])
+def test_fused_backward_matches_two_launch_backward(dev, B, T, C, H):
+    """The default backward takes one fused launch for T <= 256 (dK/dV work
+    items store the dS tiles, dQ items start on a query block once its
+    completion counter is full) and the two-launch form beyond; path 3 forces
+    the two-launch form. Both against the oracle on (b, h) slices, and against
+    each other on the whole tensor (other summation orders of dK and dV:
+    fp32 rounding only). T = 257 is past the fused kernel's limit (both paths
+    then run the same kernels, bit for bit)."""
+    x = synth.qkv(B, T, C, seed=300 + T)
+    g = synth.grad_out(B, T, C, seed=300 + T)
+    y, lse = gpu_fwd(dev, x, H)
+    gx, D = gpu_bwd(dev, x, y, lse, g, H)
+    prev = gpt_amd.set_path(3)
+    try:
+        gx3, D3 = gpu_bwd(dev, x, y, lse, g, H)
+    finally:
+        gpt_amd.set_path(prev)
+    assert np.isfinite(gx).all() and np.isfinite(D).all()
+    for name, sl in (("dQ", slice(0, C)), ("dK", slice(C, 2 * C)), ("dV", slice(2 * C, 3 * C))):
+        assert_close(f"fused vs two-launch {name} T={T}", gx[..., sl], gx3[..., sl], 1e-5)
+    assert np.array_equal(D, D3)
+    if T > 256:
+        assert np.array_equal(gx.view(np.uint32), gx3.view(np.uint32))
+    for (b, h) in {(0, 0), (B - 1, H - 1)}:
+        xs = qkv_slice(x, b, h, H)
+        gr, _ = pyoracle.backward(xs, row_slice(y, b, h, H), np.ascontiguousarray(lse[b:b + 1, :, h:h + 1]),
+                                  row_slice(g, b, h, H), 1)
+        d = C // H
+        cols = np.r_[h * d:(h + 1) * d, C + h * d:C + (h + 1) * d, 2 * C + h * d:2 * C + (h + 1) * d]
+        assert_close(f"fused T={T} (b,h)=({b},{h})", gx[b:b + 1, :, cols], gr, BWD_RTOL)
+
+
+def test_fused_backward_repeatable_across_shapes(dev):
+    """The fused backward's control block is all zeros between launches (every
+    completion counter is reset by the dQ item that used it): interleaving
+    shapes that lay out their counters differently changes nothing, bit for
+    bit, and a dQ item never reads a tile before it is complete."""
+    import torch
+
+    shapes = [(16, 256, 768, 12), (3, 100, 768, 12), (1, 200, 64, 1), (8, 256, 768, 12)]
+    data = {}
+    for (B, T, C, H) in shapes:
+        x = _to(dev, synth.qkv(B, T, C, seed=400 + B))
+        g = _to(dev, synth.grad_out(B, T, C, seed=400 + B))
+        y, lse = gpt_amd.attention_forward(x, H)
+        data[(B, T, C, H)] = (x, g, y, lse)
+    first = {}
+    for rnd in range(4):
+        for key in (shapes if rnd % 2 == 0 else shapes[::-1]):
+            B, T, C, H = key
+            x, g, y, lse = data[key]
+            gx = torch.full((B, T, 3 * C), float("nan"), device=dev)
+            D = torch.full((B, T, H), float("nan"), device=dev)
+            gpt_amd.device_flash_attention_backward(gx, D, lse, g, y, x, B, T, C, H)
+            torch.cuda.synchronize()
+            if key not in first:
+                assert torch.isfinite(gx).all()
+                first[key] = gx.clone()
+            else:
+                assert torch.equal(first[key], gx), f"run {rnd} differs at {key}"
+
+
 def test_general_path_agrees_with_mfma_path(dev):
     B, T, C, H = 2, 200, 256, 4
     x = synth.qkv(B, T, C, seed=11)
@@ -394,8 +458,9 @@ def test_batch_slices_are_independent(dev):
 
 @pytest.mark.parametrize("T", [100, 300])
 def test_launch_timer_counts_each_kernel(dev, T):
-    """One launch per kernel; up to T = 256 the dK/dV kernel computes the D
-    rows itself, longer rows take the separate D-row kernel."""
+    """One launch per kernel: up to T = 256 the backward is the one fused
+    kernel (D rows, dK/dV, dS tiles and dQ); longer rows take the D-row
+    kernel, the dK/dV kernel and the dQ kernel."""
     import torch
 
     B, C, H = 2, 768, 12
@@ -409,9 +474,10 @@ def test_launch_timer_counts_each_kernel(dev, T):
         t = gpt_amd.timing_read()
     finally:
         gpt_amd.timing_enable(False)
-    for k in ("fwd", "bwd_dkdv", "bwd_dq"):
+    kinds = ("fwd", "bwd_fused") if T <= 256 else ("fwd", "bwd_rowdot", "bwd_dkdv", "bwd_dq")
+    for k in kinds:
         ms, n = t[k]
         assert n == 1 and ms > 0, (k, t[k])
-    assert t["bwd_rowdot"][1] == (0 if T <= 256 else 1), t
-    assert t["other"] == (0.0, 0)
+    for k in set(gpt_amd.attention.KERNEL_KINDS) - set(kinds):
+        assert t[k] == (0.0, 0), (k, t[k])
     assert gpt_amd.timing_read()["fwd"] == (0.0, 0)  # read forgets
