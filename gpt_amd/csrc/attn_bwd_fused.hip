@@ -561,6 +561,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
             item = r * n_cu + c;
         }
         const int J = item / BHc, bhl = item % BHc;
+        // Wave priority by lightness: the arbiter otherwise favours the older
+        // (heavier, dispatched first) items, so that every key group finished
+        // its dK/dV item at about the same time and the dQ items ran after
+        // all of them (a timestamp trace at B=16 T=256: dK/dV items ending at
+        // 34-40 us, dQ items from 37 to 58 us). Light key groups first lets
+        // them reach their dQ items while the heavy ones are still running
+        // (12-layer step 1.0410 -> 1.0376 ms, A/B on one box).
+        {
+            const int pr = n_kg - 1 - J;
+            if (pr >= 3)
+                __builtin_amdgcn_s_setprio(3);
+            else if (pr == 2)
+                __builtin_amdgcn_s_setprio(2);
+            else if (pr == 1)
+                __builtin_amdgcn_s_setprio(1);
+        }
         dkdv_item(J, bhl);
         // the dQ blocks of this (b, h) that fall to key group J (see above)
         int load[kMaxFusedKeyGroups];
