@@ -17,6 +17,7 @@ import pytest
 
 from gpt_amd import synth
 from oracle import pyoracle
+from tests import dense64
 
 SHAPES = [
     # B, T, C, H
@@ -35,44 +36,26 @@ def _inputs(B, T, C, H, seed=7):
     return x, g
 
 
-def dense_forward64(qkv, H):
-    """Independent fp64 restatement: dense masked softmax over [T, T]."""
-    B, T, W = qkv.shape
-    C = W // 3
-    d = C // H
-    x = qkv.astype(np.float64).reshape(B, T, 3, H, d).transpose(2, 0, 3, 1, 4)  # 3,B,H,T,d
-    q, k, v = x
-    s = q @ k.transpose(0, 1, 3, 2) / np.sqrt(d)
-    mask = np.triu(np.ones((T, T), bool), 1)
-    s = np.where(mask, -np.inf, s)
-    m = s.max(-1, keepdims=True)
-    p = np.exp(s - m)
-    z = p.sum(-1, keepdims=True)
-    o = (p / z) @ v
-    lse = (m + np.log(z))[..., 0]  # B,H,T
-    return o.transpose(0, 2, 1, 3).reshape(B, T, C), lse.transpose(0, 2, 1)
+dense_forward64 = dense64.forward_np
+dense_backward64 = dense64.backward_np
 
 
-def dense_backward64(qkv, dy, H):
-    B, T, W = qkv.shape
-    C = W // 3
-    d = C // H
-    x = qkv.astype(np.float64).reshape(B, T, 3, H, d).transpose(2, 0, 3, 1, 4)
-    q, k, v = x
-    do = dy.astype(np.float64).reshape(B, T, H, d).transpose(0, 2, 1, 3)
-    s = q @ k.transpose(0, 1, 3, 2) / np.sqrt(d)
-    s = np.where(np.triu(np.ones((T, T), bool), 1), -np.inf, s)
-    p = np.exp(s - s.max(-1, keepdims=True))
-    p /= p.sum(-1, keepdims=True)
-    o = p @ v
-    dv = p.transpose(0, 1, 3, 2) @ do
-    dp = do @ v.transpose(0, 1, 3, 2)
-    Dr = (do * o).sum(-1, keepdims=True)
-    ds = p * (dp - Dr) / np.sqrt(d)
-    dq = ds @ k
-    dk = ds.transpose(0, 1, 3, 2) @ q
-    g = np.stack([dq, dk, dv])  # 3,B,H,T,d
-    return g.transpose(1, 3, 0, 2, 4).reshape(B, T, 3 * C), Dr[..., 0].transpose(0, 2, 1)
+@pytest.mark.parametrize("B,T,C,H", [(1, 1, 64, 1), (2, 37, 128, 2), (1, 70, 192, 3), (3, 64, 32, 4)])
+def test_dense64_torch_matches_numpy(B, T, C, H):
+    """The torch float64 restatement the GPU tests run on the device (whole
+    configurations) computes what the numpy one (pinned above and below)
+    does, on the CPU, to float64 rounding; with a chunk smaller than B * H the
+    (b, h) chunking is exercised too."""
+    import torch
+
+    x, g = _inputs(B, T, C, H, seed=19)
+    yr, lr = dense_forward64(x, H)
+    gr, Dr = dense_backward64(x, g, H)
+    y, lse, gx, D = dense64.fwd_bwd_torch(torch.from_numpy(x), torch.from_numpy(g), H, chunk=max(1, B * H // 2))
+    for a, r in ((y, yr), (lse, lr), (gx, gr), (D, Dr)):
+        a = a.numpy()
+        assert a.shape == r.shape
+        assert np.abs(a - r).max() <= 1e-12 * max(1.0, np.abs(r).max())
 
 
 @pytest.mark.parametrize("B,T,C,H", SHAPES)

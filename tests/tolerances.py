@@ -1,19 +1,42 @@
-"""Parity metric and tolerances shared by the tests.
+"""Parity metrics and tolerances shared by the tests.
 
 The north-star tolerance is "1e-5 relative (forward), 1e-4 relative
-(backward), fp32". Relative error of a tensor x against a reference r is
-measured norm-wise:
+(backward), fp32". Every comparison of a tensor x with a reference r applies
+two gates, and reports both numbers:
 
-    rel_err(x, r) = max_i |x_i - r_i| / max_i |r_i|
+  norm-wise     rel_err(x, r) = max_i |x_i - r_i| / max_i |r_i|  <= rtol
 
-Elementwise |x_i - r_i| / |r_i| is not used as the gate because reference
-entries near zero (an LSE that happens to be ~0, a dQ entry produced by
-heavy cancellation) make it meaningless; it is reported in messages only.
+  elementwise   |x_i - r_i| <= rtol * |r_i| + ELEM_ATOL_FRAC * rtol * max_j |r_j|
+                for all i (reported as the largest (|x_i - r_i| - rtol |r_i|) /
+                max|r|, which must stay <= ELEM_ATOL_FRAC * rtol)
+
+The elementwise gate keeps a small absolute term because entries near zero (an
+output element produced by cancellation) carry the rounding error of the
+whole sum that formed them, not of their own size. The term is a tenth of
+rtol times the largest entry: 1e-6 max|r| for the forward (about 16 fp32 ulps
+at that scale), 1e-5 max|r| for the backward. A tighter rtol * 1e-2 would
+reject correct results: the reference CPU backend's own fp32 forward
+(cpu_backend.cpp:289-356, restated by oracle/attn_oracle.c) needs 1.4e-7 max|r|
+against a float64 evaluation at B=1 T=256 H=12, and at T=257 the MFMA
+backward's dQ differs from that fp32 oracle's by 1.07e-6 max|r| at a
+near-zero entry (two fp32 sums of up to 257 terms in different orders). An
+error confined to small but real entries (a wrong mask, a dropped term) is
+still orders of magnitude above either term.
+
+Measured over the whole attention GPU suite (570 comparisons): the largest
+excess is 7.4e-7 max|r| for the forward and 1.1e-6 max|r| for the backward,
+except in two deliberately extreme tests, which pass a looser term of
+0.5 rtol max|r| (elem_frac) and say why: scores that jump by 50 mid-row
+(dQ 2.6e-5, O 2.1e-6) and single rows of 32736 and 32800 keys checked against
+float64 (O 2.7e-6).
 """
+import os
+
 import numpy as np
 
 FWD_RTOL = 1e-5
 BWD_RTOL = 1e-4
+ELEM_ATOL_FRAC = 0.1
 
 
 def rel_err(x, r) -> float:
@@ -27,7 +50,34 @@ def rel_err(x, r) -> float:
     return float(num / denom) if denom > 0 else float(num)
 
 
-def assert_close(name: str, x, r, rtol: float) -> float:
+def elem_excess(x, r, rtol: float) -> float:
+    """max_i (|x_i - r_i| - rtol |r_i|) / max|r|: the absolute term (as a
+    fraction of max|r|) that the elementwise gate needs; <= ELEM_ATOL_FRAC *
+    rtol passes."""
+    x = np.asarray(x, dtype=np.float64)
+    r = np.asarray(r, dtype=np.float64)
+    assert x.shape == r.shape, (x.shape, r.shape)
+    if not np.all(np.isfinite(x)):
+        return float("inf")
+    if r.size == 0:
+        return 0.0
+    denom = np.max(np.abs(r))
+    excess = np.max(np.abs(x - r) - rtol * np.abs(r))
+    return float(excess / denom) if denom > 0 else float(excess)
+
+
+def assert_close(name: str, x, r, rtol: float, elementwise: bool = True,
+                 elem_frac: float = ELEM_ATOL_FRAC) -> float:
+    """Both gates (the elementwise one only if `elementwise`, with absolute
+    term elem_frac * rtol * max|r|); prints both numbers and returns the
+    norm-wise error."""
     e = rel_err(x, r)
-    assert e <= rtol, f"{name}: rel_err {e:.3e} > {rtol:.0e}"
+    ex = elem_excess(x, r, rtol)
+    atol = elem_frac * rtol
+    print(f"{name}: rel_err {e:.3e} (<= {rtol:.0e}), elementwise excess {ex:.3e}"
+          + (f" (<= {atol:.0e})" if elementwise else " (not gated)"))
+    assert e <= rtol, f"{name}: rel_err {e:.3e} > {rtol:.0e} (elementwise excess {ex:.3e})"
+    if elementwise and not os.environ.get("GPT_AMD_ELEM_REPORT_ONLY"):
+        assert ex <= atol, (f"{name}: elementwise |x-r| > {rtol:.0e}|r| + {atol:.0e} max|r| "
+                            f"(excess {ex:.3e})")
     return e
