@@ -36,6 +36,11 @@ Usage:
                                                             for every prefix T=1..256 (the reference's
                                                             generation loop without a KV cache); one
                                                             JSON line of its own
+  python bench.py --configs [--no-cpu]                      BASELINE configs 1, 2, 4 and 5(a): one JSON
+                                                            line each (GPU time, TFLOP/s, % peak,
+                                                            per-kernel times; CPU baseline on 1 core
+                                                            and on N threads, with the errors of the
+                                                            GPU outputs on its sampled (b, h))
   python bench.py --ops [--no-cpu]                          the GPT-2 124M ops around attention
                                                             (gpt_amd/libgpt_hip_ops.so) at the C3
                                                             shapes, each against its roofline; one
@@ -135,6 +140,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--prefix-sweep", action="store_true",
                     help="time BASELINE config 5(b) (forward, B=1, T=1..256) instead of the headline")
+    ap.add_argument("--configs", action="store_true",
+                    help="time BASELINE configs 1, 2, 4 and 5(a), one JSON line each")
+    ap.add_argument("--only", default="", help="with --configs: a comma-separated subset, e.g. C4,C5a")
     ap.add_argument("--ops", action="store_true",
                     help="time the GPT-2 ops around attention (libgpt_hip_ops.so) instead of the headline")
     ap.add_argument("--bwd-path", type=int, default=0, choices=(0, 2, 3),
@@ -145,7 +153,12 @@ def parse():
 
 def cpu_baseline(layers: int):
     """Reference CPUBackend attention fwd+bwd on `layers` layers of the same
-    workload (B=16, T=256), single thread; returns the cpu_baseline object."""
+    workload (B=16, T=256): once on 1 thread (the reference as written), once
+    on N = min(B, 16, cpu_count) threads, one batch element per thread calling
+    the unchanged function with B=1 on that element's slice (its batch loop is
+    independent per element). value = the N-thread rate; value_1core beside."""
+    import threading
+
     import numpy as np
 
     from gpt_amd import synth
@@ -153,24 +166,43 @@ def cpu_baseline(layers: int):
 
     impl, kind = ("ref_fast", "reference") if pyoracle.ref_available(fast=True) else ("oracle", "port")
     scales = synth.layer_scales(LAYERS, CONFIG_SEED)
-    total = 0.0
+    data = []
     for layer in range(layers):
         seed = CONFIG_SEED + layer
-        x = synth.qkv(B, T, C, seed, scale=float(scales[layer]))
-        g = synth.grad_out(B, T, C, seed)
-        t0 = time.perf_counter()
+        data.append((synth.qkv(B, T, C, seed, scale=float(scales[layer])), synth.grad_out(B, T, C, seed)))
+
+    def run(x, g):
         y, lse = pyoracle.forward(x, H, impl)
         pyoracle.backward(x, y, lse, g, H, impl)
-        total += time.perf_counter() - t0
         assert np.isfinite(y).all()
+
+    t0 = time.perf_counter()
+    for x, g in data:
+        run(x, g)
+    t1 = time.perf_counter() - t0
+    n_thr = max(1, min(B, 16, os.cpu_count() or 1))
+    t0 = time.perf_counter()
+    for x, g in data:
+        for b0 in range(0, B, n_thr):
+            ths = [threading.Thread(target=run, args=(np.ascontiguousarray(x[b:b + 1]), np.ascontiguousarray(g[b:b + 1])))
+                   for b in range(b0, min(B, b0 + n_thr))]
+            for th in ths:
+                th.start()
+            for th in ths:
+                th.join()
+    tn = time.perf_counter() - t0
     flops = layers * attn_flops(B, T, H, D_HEAD)
+    lib = "oracle/_ref/libref_cpu_attn_fast.so, -O3 -march=x86-64-v3" if kind == "reference" else "oracle/liboracle_attn.so"
     return {
-        "value": round(flops / total / 1e12, 6),
+        "value": round(flops / tn / 1e12, 6),
         "unit": "TFLOP/s",
-        "cores": 1,
+        "cores": n_thr,
+        "value_1core": round(flops / t1 / 1e12, 6),
+        "nproc": os.cpu_count(),
+        "cpu_model": _cpu_model(),
         "kind": kind,
-        "sample": f"{layers} of the 12 layers (B=16,T=256,H=12,d=64) fwd+bwd, "
-                  f"{total:.2f} s on 1 thread ({'oracle/_ref/libref_cpu_attn_fast.so, -O3' if kind == 'reference' else 'oracle/liboracle_attn.so'})",
+        "sample": f"{layers} of the 12 layers (B=16,T=256,H=12,d=64) fwd+bwd: {t1:.2f} s on 1 thread, "
+                  f"{tn:.2f} s on {n_thr} threads (one batch element each) ({lib})",
     }
 
 
@@ -250,6 +282,192 @@ def prefix_sweep(args):
         out["cpu_baseline"] = {"value": round(flops / cpu_s / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": kind,
                                "sample": f"the whole sweep, {cpu_s:.2f} s on 1 thread"}
     print(json.dumps(out), flush=True)
+
+
+# BASELINE configs other than the headline (3) and the prefix sweep (5b):
+# (name, B, T, backward, seed = 1234 + config index, GPU reps, CPU sample as
+# (batch elements, heads per element)). The CPU sample is bounded to a few
+# seconds of one core: the whole config for C1 and C2, 2 of the 12 heads of
+# every batch element for C4, 1 head of each of the 2 batch elements for C5a.
+CONFIG_LIST = [
+    ("C1", 1, 256, False, 1235, 50, (1, 12)),
+    ("C2", 8, 256, True, 1236, 30, (8, 12)),
+    ("C4", 8, 1024, True, 1238, 20, (8, 2)),
+    ("C5a", 2, 4096, True, 1239, 5, (2, 1)),
+]
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_leg(x, g, H, bwd, sample, gpu_out):
+    """The reference CPU backend (oracle/_ref, -O3; the C restatement if that
+    is not built) on `sample` = (n_b, n_h): heads 0, H-1, ... of the first n_b
+    batch elements, each element's heads as one call with B=1 on a compacted
+    qkv (the unchanged function on a smaller tensor). Timed on 1 thread, then
+    on N = min(n_b, 16, cpu_count) threads (one batch element each: the
+    reference's batch loop is independent per element, so the results are
+    identical). The GPU outputs on the same (b, h) are compared with the CPU
+    ones (norm-wise and elementwise, tests/tolerances.py's metrics)."""
+    import threading
+
+    import numpy as np
+
+    from oracle import pyoracle
+
+    impl, kind = ("ref_fast", "reference") if pyoracle.ref_available(fast=True) else ("oracle", "port")
+    B, T, W = x.shape
+    C = W // 3
+    d = C // H
+    n_b, n_h = sample
+    heads = sorted({round(i * (H - 1) / max(1, n_h - 1)) for i in range(n_h)}) if n_h < H else list(range(H))
+    cols_h = np.concatenate([np.arange(h * d, (h + 1) * d) for h in heads])
+    cols_qkv = np.concatenate([cols_h, C + cols_h, 2 * C + cols_h])
+    items = [(b, np.ascontiguousarray(x[b:b + 1, :, cols_qkv]), np.ascontiguousarray(g[b:b + 1, :, cols_h]))
+             for b in range(n_b)]
+    Hs = len(heads)
+    res = [None] * n_b
+
+    def work(k):
+        b, xs, gs = items[k]
+        y, lse = pyoracle.forward(xs, Hs, impl)
+        gx = D = None
+        if bwd:
+            gx, D = pyoracle.backward(xs, y, lse, gs, Hs, impl)
+        res[k] = (y, lse, gx, D)
+
+    t0 = time.perf_counter()
+    for k in range(n_b):
+        work(k)
+    t1 = time.perf_counter() - t0
+    n_thr = max(1, min(n_b, 16, os.cpu_count() or 1))
+    t0 = time.perf_counter()
+    for k0 in range(0, n_b, n_thr):
+        ths = [threading.Thread(target=work, args=(k,)) for k in range(k0, min(n_b, k0 + n_thr))]
+        for th in ths:
+            th.start()
+        for th in ths:
+            th.join()
+    tn = time.perf_counter() - t0
+    flops = n_b * Hs * d * T * (T + 1) * (7 if bwd else 2)
+
+    def errs(a, r, rtol):
+        a = a.astype(np.float64)
+        r = r.astype(np.float64)
+        m = np.abs(r).max()
+        return {"rel": float(np.abs(a - r).max() / m), "elem_excess": float((np.abs(a - r) - rtol * np.abs(r)).max() / m)}
+
+    ygpu, lgpu, gxgpu, Dgpu = gpu_out
+    e = {}
+    for k, (b, _, _) in enumerate(items):
+        y, lse, gx, D = res[k]
+        cur = {"O": errs(ygpu[b:b + 1, :, cols_h], y, 1e-5), "LSE": errs(lgpu[b:b + 1, :, heads], lse, 1e-5)}
+        if bwd:
+            for nm, off in (("dQ", 0), ("dK", 1), ("dV", 2)):
+                sel = slice(off * Hs * d, (off + 1) * Hs * d)
+                cur[nm] = errs(gxgpu[b:b + 1, :, off * C + cols_h], gx[..., sel], 1e-4)
+            cur["D"] = errs(Dgpu[b:b + 1, :, heads], D, 1e-4)
+        for nm, v in cur.items():
+            if nm not in e:
+                e[nm] = v
+            else:
+                e[nm] = {kk: max(e[nm][kk], v[kk]) for kk in v}
+    return {
+        "value_1core": round(flops / t1 / 1e12, 6),
+        "value_ncore": round(flops / tn / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": [1, n_thr],
+        "nproc": os.cpu_count(),
+        "cpu_model": _cpu_model(),
+        "kind": kind,
+        "sample": f"{n_b} batch element(s) x heads {heads} of B={B} T={T} H={H}, "
+                  f"{'fwd+bwd' if bwd else 'fwd'}: {t1:.2f} s on 1 thread, {tn:.2f} s on {n_thr}",
+        "gpu_vs_cpu_on_sample": {k: {kk: float(f"{vv:.3e}") for kk, vv in v.items()} for k, v in e.items()},
+    }
+
+
+def configs_bench(args):
+    """BASELINE configs 1, 2, 4 and 5(a) (BASELINE.md "Results"): per config,
+    the forward (C1) or forward + backward through the C ABI on resident
+    inputs, K calls back to back between two events (after 3 warm-up calls),
+    value = algorithmic FLOPs / time per call; per-kernel averages from the
+    library's launch timer in a second pass; the CPU baseline leg on a
+    bounded sample, with the GPU outputs' errors on it."""
+    import numpy as np
+    import torch
+
+    import gpt_amd
+    from gpt_amd import synth
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    if args.bwd_path:
+        gpt_amd.set_path(args.bwd_path)
+    only = set(args.only.split(",")) if args.only else None
+    for name, Bc, Tc, bwd, seed, reps, sample in CONFIG_LIST:
+        if only and name not in only:
+            continue
+        x = synth.qkv(Bc, Tc, C, seed)
+        g = synth.grad_out(Bc, Tc, C, seed)
+        xd, gd = torch.from_numpy(x).to(dev), torch.from_numpy(g).to(dev)
+        y = torch.empty(Bc, Tc, C, device=dev)
+        lse = torch.empty(Bc, Tc, H, device=dev)
+        gx = torch.empty(Bc, Tc, 3 * C, device=dev)
+        Dd = torch.empty(Bc, Tc, H, device=dev)
+
+        def call():
+            gpt_amd.device_flash_attention_forward(y, lse, xd, Bc, Tc, C, H, stream)
+            if bwd:
+                gpt_amd.device_flash_attention_backward(gx, Dd, lse, gd, y, xd, Bc, Tc, C, H, stream)
+
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        gpt_amd.timing_enable(True)
+        for _ in range(reps):
+            call()
+        torch.cuda.synchronize()
+        per_kernel = gpt_amd.timing_read()
+        gpt_amd.timing_enable(False)
+        flops = attn_flops(Bc, Tc, H, D_HEAD, bwd=bwd)
+        tf = flops / (ms * 1e-3) / 1e12
+        out = {
+            "metric": f"causal attn {'fwd+bwd' if bwd else 'fwd'} TFLOP/s & % fp32 MFMA peak, "
+                      f"BASELINE config {name[1:]}, 1 GPU",
+            "value": round(tf, 3),
+            "unit": "TFLOP/s",
+            "n_gpus": 1,
+            "higher_is_better": True,
+            "dtype": "fp32",
+            "data": "synthetic (splitmix64 Box-Muller; Q/K/V ~ N(0,1), dO ~ N(0,1e-3))",
+            "config": {"workload": f"BASELINE config {name[1:]}: causal {'fwd+bwd' if bwd else 'fwd'}, "
+                                   f"B={Bc} T={Tc} H={H} d={D_HEAD}", "flops_per_call": flops, "reps": reps},
+            "ms_per_call": round(ms, 5),
+            **({"bwd_path": args.bwd_path} if args.bwd_path else {}),
+            "pct_fp32_mfma_peak": round(100 * tf / PEAK_FP32_MFMA_TFLOPS, 2),
+            "kernels": {k: {"avg_us": round(1e3 * t / n, 3), "launches": n} for k, (t, n) in per_kernel.items()
+                        if n > 0},
+        }
+        if not args.no_cpu:
+            torch.cuda.synchronize()
+            gpu_out = (y.cpu().numpy(), lse.cpu().numpy(), gx.cpu().numpy() if bwd else None,
+                       Dd.cpu().numpy() if bwd else None)
+            out["cpu_baseline"] = _cpu_leg(x, g, H, bwd, sample, gpu_out)
+        print(json.dumps(out), flush=True)
 
 
 # GPT-2 124M around the attention path at the C3 shapes (B=16, T=256): d_model
@@ -500,6 +718,9 @@ def main():
         return
     if args.ops:
         ops_bench(args)
+        return
+    if args.configs:
+        configs_bench(args)
         return
 
     import numpy as np

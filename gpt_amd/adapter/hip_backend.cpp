@@ -38,13 +38,26 @@ void die_ops(int rc)
 
 }  // namespace
 
-HipBackend::HipBackend(unsigned long seed) : seed_(seed)
+HipBackend::HipBackend(unsigned long seed) : seed_(seed), pool_(new Pool)
 {
     if (!gpt_hip_attn_device_ok())
     {
         std::fprintf(stderr, "[hip_backend] no usable HIP device\n");
         std::abort();
     }
+}
+
+HipBackend::~HipBackend()
+{
+    // the pooled blocks go back to the runtime; blocks still handed out
+    // belong to the caller, whose later device_free calls go straight to
+    // hipFree (the pool object itself is kept for them)
+    pool_->released = true;
+    if (hipDeviceSynchronize() != hipSuccess)
+        return;
+    for (auto &kv : pool_->free_blocks)
+        (void)hipFree(kv.second);
+    pool_->free_blocks.clear();
 }
 
 void HipBackend::device_get_memory_info(float *free_mb, float *total_mb)
@@ -55,9 +68,73 @@ void HipBackend::device_get_memory_info(float *free_mb, float *total_mb)
     *total_mb = (float)(t / (1024.0 * 1024.0));
 }
 
-void HipBackend::device_malloc(void **ptr, size_t size) { die_hip(hipMalloc(ptr, size), "hipMalloc"); }
+// Caching allocation pool. The reference's generator re-sizes the model every
+// token: GPT::set_size frees every activation buffer and allocates it again
+// for the new prefix length (src/model/gpt.cpp:399-424, called from
+// src/infer/infer.cpp:116-118). On the HIP runtime each hipFree waits for the
+// device and each hipMalloc maps fresh memory, so here a freed block goes to a
+// free list by its bucket size and the next request of that bucket takes it
+// back: sizes are rounded up to a power of two from 256 bytes to 1 GiB (a
+// prefix that grows by one token stays in its buckets), to a multiple of
+// 256 MiB beyond. Reuse is safe without waiting: every op of this backend runs
+// on the legacy default stream, in order, so work queued on a block before it
+// was freed runs before work queued after it was handed out again. Memory goes
+// back to the runtime only when the backend is destroyed.
+static size_t pool_bucket(size_t n)
+{
+    constexpr size_t kMinBucket = 256, kPow2Max = size_t(1) << 30, kLargeStep = size_t(256) << 20;
+    if (n <= kMinBucket)
+        return kMinBucket;
+    if (n > kPow2Max)
+        return (n + kLargeStep - 1) / kLargeStep * kLargeStep;
+    size_t b = kMinBucket;
+    while (b < n)
+        b <<= 1;
+    return b;
+}
 
-void HipBackend::device_free(void *ptr) { die_hip(hipFree(ptr), "hipFree"); }
+void HipBackend::device_malloc(void **ptr, size_t size)
+{
+    Pool &p = *pool_;
+    ++p.mallocs;
+    if (p.released)
+    {
+        die_hip(hipMalloc(ptr, size), "hipMalloc");
+        return;
+    }
+    const size_t b = pool_bucket(size);
+    auto it = p.free_blocks.find(b);
+    if (it != p.free_blocks.end())
+    {
+        *ptr = it->second;
+        p.free_blocks.erase(it);
+        ++p.reused;
+    }
+    else
+    {
+        die_hip(hipMalloc(ptr, b), "hipMalloc");
+        p.held += b;
+    }
+    p.block_bytes[*ptr] = b;
+}
+
+void HipBackend::device_free(void *ptr)
+{
+    if (!ptr)
+        return;
+    Pool &p = *pool_;
+    auto it = p.block_bytes.find(ptr);
+    if (it == p.block_bytes.end() || p.released)
+    {
+        // after the destructor (or a block from before it): straight back
+        if (it != p.block_bytes.end())
+            p.block_bytes.erase(it);
+        die_hip(hipFree(ptr), "hipFree");
+        return;
+    }
+    p.free_blocks.emplace(it->second, ptr);
+    p.block_bytes.erase(it);
+}
 
 void HipBackend::device_memset(void *ptr, int value, size_t size) { die_hip(hipMemset(ptr, value, size), "hipMemset"); }
 

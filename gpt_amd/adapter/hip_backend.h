@@ -12,12 +12,14 @@
 #include "backend_interface.h"
 
 #include <cstddef>
+#include <map>
+#include <unordered_map>
 
 class HipBackend : public IGPTBackend
 {
 public:
     explicit HipBackend(unsigned long seed = 42);
-    ~HipBackend() override = default;
+    ~HipBackend() override;
 
     void device_get_memory_info(float *free_mb, float *total_mb) override;
     void device_malloc(void **ptr, size_t size) override;
@@ -67,7 +69,31 @@ public:
                            float eps, float weight_decay, int step) override;
     void device_scale_and_clip_grad(float *g, int size, float max_norm, int accum_steps) override;
 
+    // Allocation pool statistics: device_malloc calls, of which served from
+    // the pool, and the bytes the pool holds from the HIP runtime.
+    struct PoolStats
+    {
+        size_t mallocs, reused, bytes_held;
+    };
+    PoolStats pool_stats() const { return {pool_->mallocs, pool_->reused, pool_->held}; }
+
 private:
     unsigned long long seed_;
     unsigned long long fills_ = 0;  // fill_normal calls so far: each draws a fresh stream
+    // Caching allocation pool (see device_malloc): freed blocks by bucket
+    // size, and the bucket size of every block handed out. On the heap and
+    // never deleted: the reference's trainer and generator delete their
+    // backend (src/train/train.cpp:165, src/infer/infer.cpp:166) before their
+    // model and data objects go out of scope and free their buffers through
+    // it (src/model/gpt.cpp:92, src/infer/data_manager.cpp:22), so the pool
+    // must outlive this object; after the destructor it passes every call
+    // straight to the HIP runtime.
+    struct Pool
+    {
+        std::multimap<size_t, void *> free_blocks;
+        std::unordered_map<void *, size_t> block_bytes;
+        size_t mallocs = 0, reused = 0, held = 0;
+        bool released = false;
+    };
+    Pool *pool_;
 };

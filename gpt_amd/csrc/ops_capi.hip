@@ -399,8 +399,13 @@ int lt_gemm(const char *op, hipStream_t st, bool ta, bool tb, int M, int N, int 
                                               q->lc, &q->algo, nullptr, 0, st);
     if (s != HIPBLAS_STATUS_SUCCESS)
     {
-        // refused before launching anything: this shape goes to rocBLAS from now on
-        q->ok = false;
+        q->ok = false;  // this shape goes to rocBLAS from now on
+        // An accumulating product (beta != 0) is not run again on rocBLAS:
+        // if the failed call had enqueued any work, a second run would add
+        // the product twice. An overwriting one (beta = 0) is safe to redo.
+        if (beta != 0.f)
+            return fail(GPT_HIP_OPS_ELAUNCH, "%s: hipblasLtMatmul failed (%d) on an accumulating product", op,
+                        (int)s);
         return 1;
     }
     return 0;
@@ -776,5 +781,30 @@ int gpt_hip_fill_const_f32(float *ptr, float value, size_t size, void *stream)
 }
 
 const char *gpt_hip_ops_last_error(void) { return g_err; }
+
+int gpt_hip_ops_gemm_info(int *plans, int *tuned, int *blaslt_version)
+{
+    if (!plans || !tuned || !blaslt_version)
+        return fail(GPT_HIP_OPS_ENULL, "gpt_hip_ops_gemm_info: NULL output");
+    std::lock_guard<std::mutex> lock(g_lt_mu);
+    int np = 0, nt = 0;
+    for (int i = 0; i < g_nplans; ++i)
+    {
+        np += g_plans[i].ok ? 1 : 0;
+        nt += g_plans[i].ok && g_plans[i].tuned ? 1 : 0;
+    }
+    *plans = np;
+    *tuned = nt;
+    *blaslt_version = 0;
+    for (int d = 0; d < kMaxDevices; ++d)
+        if (g_lt[d])
+        {
+            int v = 0;
+            if (hipblasLtGetVersion(g_lt[d], &v) == HIPBLAS_STATUS_SUCCESS)
+                *blaslt_version = v;
+            break;
+        }
+    return 0;
+}
 
 }  // extern "C"

@@ -79,6 +79,8 @@ def load_library():
             fn.restype = ctypes.c_int
         lib.gpt_hip_ops_last_error.argtypes = []
         lib.gpt_hip_ops_last_error.restype = ctypes.c_char_p
+        lib.gpt_hip_ops_gemm_info.argtypes = [ctypes.POINTER(ctypes.c_int)] * 3
+        lib.gpt_hip_ops_gemm_info.restype = ctypes.c_int
         _lib = lib
     return _lib
 
@@ -198,3 +200,15 @@ def device_fill_normal(ptr, mean, stddev, size, seed=0, stream=None):
 
 def device_fill_const(ptr, value, size, stream=None):
     _call("gpt_hip_fill_const_f32", _addr(ptr, "ptr"), value, size, _stream(stream))
+
+
+def gemm_info() -> dict:
+    """{"plans", "tuned", "blaslt_version"}: the hipBLASLt GEMM plans this
+    process has made, how many of them run the tuning table's kernel for
+    their shape, and the loaded hipBLASLt's version (0 before any plan)."""
+    lib = load_library()
+    vals = [ctypes.c_int(0) for _ in range(3)]
+    rc = lib.gpt_hip_ops_gemm_info(*[ctypes.byref(v) for v in vals])
+    if rc != 0:
+        raise HipOpsError(rc, lib.gpt_hip_ops_last_error().decode(errors="replace"))
+    return {"plans": vals[0].value, "tuned": vals[1].value, "blaslt_version": vals[2].value}

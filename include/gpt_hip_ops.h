@@ -176,6 +176,14 @@ int gpt_hip_fill_const_f32(float *ptr, float value, size_t size, void *stream);
  * No reference counterpart (the reference prints and aborts). */
 const char *gpt_hip_ops_last_error(void);
 
+/* GEMM planning state, for tests and tuning: *plans = hipBLASLt plans in use
+ * (one per shape, transposes and epilogue taken so far in this process),
+ * *tuned = how many of them run the kernel this library's tuning table names
+ * for the shape (GPT-2 124M's linear layers at 4096 rows, on the two
+ * hipBLASLt builds the table covers), *blaslt_version = the loaded hipBLASLt's
+ * hipblasLtGetVersion (0 before the first plan). No reference counterpart. */
+int gpt_hip_ops_gemm_info(int *plans, int *tuned, int *blaslt_version);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,4 +45,13 @@ def test_reference_generator_runs_gpt2_124m_on_the_gpu(tmp_path, dev):
     assert np.all(out < 50257)
     fwd = re.search(r"Average forward pass time: ([0-9.]+) ms", r.stdout)
     assert fwd, r.stdout[-1000:]
-    print(f"GPT-2 124M generation, prefix 33..80: {float(fwd.group(1)):.2f} ms per forward pass (incl. set_size)")
+    # the program's own per-step scopes (infer.cpp:116-124): Preparation is
+    # gpt.set_size (every activation freed and allocated again for the new
+    # prefix length), ForwardPass the forward plus the copy of the last row of
+    # logits; the averages cover every step, the 5 warm-up steps included
+    prep = [float(v) for v in re.findall(r"Preparation took ([0-9.]+) ms", r.stdout)]
+    fp = [float(v) for v in re.findall(r"ForwardPass took ([0-9.]+) ms", r.stdout)]
+    assert prep and fp and len(prep) == len(fp)
+    print(f"GPT-2 124M generation, prefix 33..80: average forward pass {float(fwd.group(1)):.2f} ms; "
+          f"per step (all {len(fp)} steps): Preparation {np.mean(prep):.3f} ms (median {np.median(prep):.3f}), "
+          f"ForwardPass {np.mean(fp):.3f} ms (median {np.median(fp):.3f})")

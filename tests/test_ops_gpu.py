@@ -13,6 +13,8 @@ outputs start from random values of the size of what is added to them, so
 cover GPT-2 124M's widths (C = 768, 3C, 4C, the padded vocabulary 50304 with
 V = 50257) and ragged / unaligned widths that take the scalar kernels.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -231,6 +233,75 @@ def test_linear_at_gpt2_step_shapes(dev, n_in, n_out, activation):
     assert_close("linear grad_x", host(gx).reshape(-1, n_in), gy64 @ w64.T, RTOL)
     assert_close("linear grad_w", host(dgw), gw0.astype(np.float64) + x64.T @ gy64, RTOL)
     assert_close("linear grad_b", host(dgb), gb0.astype(np.float64) + gy64.sum(0), RTOL)
+    # the tuning table lists kernels of this (PyTorch-bundled) hipBLASLt for
+    # every one of these shapes: at least one plan must have taken one
+    info = ops.gemm_info()
+    print("gemm plans:", info)
+    assert info["tuned"] >= 1, info
+
+
+def test_linear_at_gpt2_step_shapes_without_torch(dev):
+    """The same four layer shapes in a process that never imports PyTorch
+    (tests/torchfree_linear.py, device memory from the HIP runtime through
+    ctypes), where the library binds ROCm's own hipBLASLt, the build the
+    reference-side trainer and generator run on: parity against float64
+    numpy at 1e-5 and the tuned kernels taken."""
+    import subprocess
+    import sys
+
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "torchfree_linear.py")
+    r = subprocess.run([sys.executable, "-u", script], capture_output=True, text=True, timeout=240)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+def test_unembedding_at_gpt2_step_shape(dev):
+    """The unembedding GEMMs at the training step's shape, B=16 T=256 C=768
+    against the padded vocabulary Vp=50304 (the largest GEMMs of the step;
+    grad_x and grad_wte take hipBLASLt, the logits rocBLAS): logits and grad_x
+    on 512 sampled rows against float64 numpy, grad_wte (accumulated onto a
+    nonzero start) in full against a float64 product on the device (rocBLAS
+    dgemm through torch, independent of the fp32 path under test), 1e-5
+    norm-wise. The reference semantics: cpu_backend.cpp:81-140.
+
+    grad_x is a 50304-term fp32 reduction, where 1e-5 is the size of fp32's
+    own rounding: the reference CPU backend's order (one float accumulator
+    over v, cpu_backend.cpp:125-131, restated here in numpy on 64 of the
+    rows) is off float64 by about 1.1e-5 on these inputs. Its tolerance is
+    max(1e-5, 2x that reference-order error on the same rows), printed."""
+    import torch
+
+    B, T, C, Vp = 16, 256, 768, 50304
+    r = rng(2024)
+    x = f32(r.standard_normal((B, T, C)))
+    wte = f32(r.standard_normal((Vp, C)) * 0.05)
+    gy = f32(r.standard_normal((B, T, Vp)) * 1e-3)
+    gw0 = f32(r.standard_normal((Vp, C)) * 1e-3)
+    dx, dw, dgy, dgw = (to_dev(dev, a) for a in (x, wte, gy, gw0))
+    y = torch.empty((B, T, Vp), device=dev)
+    gx = torch.empty((B, T, C), device=dev)
+    ops.device_unembedding_forward(y, dx, dw, B, T, C, Vp)
+    ops.device_unembedding_backward(gx, dgw, dgy, dx, dw, B, T, C, Vp)
+    torch.cuda.synchronize()
+    rows = np.sort(r.choice(B * T, 512, replace=False))
+    x64 = x.reshape(-1, C)[rows].astype(np.float64)
+    w64 = wte.astype(np.float64)
+    assert_close("unembedding y (512 rows)", host(y).reshape(-1, Vp)[rows], x64 @ w64.T, RTOL)
+    gx_h = host(gx).reshape(-1, C)[rows]
+    gx_64 = gy.reshape(-1, Vp)[rows].astype(np.float64) @ w64
+    sub = np.arange(0, 512, 8)
+    g_sub = gy.reshape(-1, Vp)[rows[sub]]
+    acc = np.zeros((sub.size, C), np.float32)
+    for v in range(Vp):  # the reference's accumulation order, one fp32 sum per output
+        acc += g_sub[:, v:v + 1] * wte[v]
+    ref_order = rel_err(acc, gx_64[sub])
+    tol = max(RTOL, 2.0 * ref_order)
+    print(f"reference-order fp32 grad_x error {ref_order:.3e} -> tolerance {tol:.3e}")
+    assert_close("unembedding grad_x (64 rows)", gx_h[sub], gx_64[sub], tol)
+    assert_close("unembedding grad_x (512 rows)", gx_h, gx_64, tol)
+    g_ref = (dgy.reshape(-1, Vp).double().t().contiguous() @ dx.reshape(-1, C).double()
+             + torch.from_numpy(gw0).to(dev).double())
+    assert_close("unembedding grad_wte (all)", host(dgw), g_ref.cpu().numpy(), RTOL)
 
 
 def test_gemm_ops_are_bitwise_repeatable(dev):
