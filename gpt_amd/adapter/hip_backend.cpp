@@ -9,6 +9,7 @@
 
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 
 namespace {
 
@@ -58,6 +59,10 @@ HipBackend::~HipBackend()
     for (auto &kv : pool_->free_blocks)
         (void)hipFree(kv.second);
     pool_->free_blocks.clear();
+    if (pool_->stage)
+        (void)hipHostFree(pool_->stage);
+    pool_->stage = nullptr;
+    pool_->stage_bytes = 0;
 }
 
 void HipBackend::device_get_memory_info(float *free_mb, float *total_mb)
@@ -150,14 +155,52 @@ void HipBackend::device_fill_const(float *ptr, float value, size_t size)
     die_ops(gpt_hip_fill_const_f32(ptr, value, size, nullptr));
 }
 
+// Host copies of up to kStageMax bytes (the generator's row of logits per
+// token, the trainer's token batches) go through a pinned buffer the backend
+// owns: a DMA into page-locked memory plus a host memcpy, instead of the
+// runtime's pageable-memory path, whose first use in a process can stall a
+// call for milliseconds. Larger copies (checkpoints) go straight through.
+void *HipBackend::stage(size_t size)
+{
+    Pool &p = *pool_;
+    if (p.released || size == 0 || size > kStageMax)
+        return nullptr;
+    if (size > p.stage_bytes)
+    {
+        size_t n = 1 << 16;
+        while (n < size)
+            n <<= 1;
+        if (p.stage)
+            die_hip(hipHostFree(p.stage), "hipHostFree");
+        p.stage = nullptr;
+        die_hip(hipHostMalloc(&p.stage, n, hipHostMallocDefault), "hipHostMalloc");
+        p.stage_bytes = n;
+    }
+    return p.stage;
+}
+
 void HipBackend::device_memcpy_d2h(void *dst, const void *src, size_t size)
 {
-    die_hip(hipMemcpy(dst, src, size, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    void *b = stage(size);
+    if (!b)
+    {
+        die_hip(hipMemcpy(dst, src, size, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+        return;
+    }
+    die_hip(hipMemcpy(b, src, size, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    std::memcpy(dst, b, size);
 }
 
 void HipBackend::device_memcpy_h2d(void *dst, const void *src, size_t size)
 {
-    die_hip(hipMemcpy(dst, src, size, hipMemcpyHostToDevice), "hipMemcpy H2D");
+    void *b = stage(size);
+    if (!b)
+    {
+        die_hip(hipMemcpy(dst, src, size, hipMemcpyHostToDevice), "hipMemcpy H2D");
+        return;
+    }
+    std::memcpy(b, src, size);
+    die_hip(hipMemcpy(dst, b, size, hipMemcpyHostToDevice), "hipMemcpy H2D");
 }
 
 void HipBackend::device_embedding_forward(float *y, const float *wte, const float *wpe, const int *input_tokens,

@@ -94,6 +94,12 @@ private:
         std::unordered_map<void *, size_t> block_bytes;
         size_t mallocs = 0, reused = 0, held = 0;
         bool released = false;
+        // pinned bounce buffer for host copies up to kStageMax bytes
+        // (grown to the largest such copy, hipHostMalloc)
+        void *stage = nullptr;
+        size_t stage_bytes = 0;
     };
+    static constexpr size_t kStageMax = size_t(64) << 20;
+    void *stage(size_t size);
     Pool *pool_;
 };
