@@ -22,13 +22,18 @@
 //     and one thread adds 1 to the completion counter of (b, h, i + 1); the
 //     last block's counter is bumped after a final wait.
 //   dQ items (b, h, query block i), done by the workgroups of the same
-//     (b, h) once their dK/dV item is done: the blocks are assigned to the
-//     key groups longest-processing-time first (from the heaviest block down,
-//     each to the key group with the least work so far, counting a dK/dV step
-//     as 8 and dQ_i as i + 1), which every workgroup computes the same way, so
-//     no queue or atomic is involved and the light key groups take the dQ
-//     work while the heavy ones are still on their own (at B=16 T=256 the
-//     heaviest key group takes none). A workgroup runs its dQ items from the
+//     (b, h) once their dK/dV item is done: the blocks are dealt to the key
+//     groups by dQ work alone, longest-processing-time first (from the
+//     heaviest block down, each to the key group with the least dQ work so
+//     far), which every workgroup computes the same way, so no queue or atomic
+//     is involved and every key group takes about the same dQ work (at B=16
+//     T=256 key groups 0..3 take blocks {4, 3}, {5, 2}, {6, 1}, {7, 0}).
+//     Weighting the dK/dV work in as well (a step as 8 units, dQ_i as i + 1)
+//     gave all the dQ work to the two lightest key groups, which under the
+//     wave priorities below end their dK/dV items no earlier than the heavy
+//     ones, so half of the workgroups ran all the dQ work after everything
+//     else (12-layer step 1.0443 -> 1.0085 ms when it went, A/B on one box).
+//     A workgroup runs its dQ items from the
 //     highest block down: wait until the counter of (b, h, i) reaches the
 //     number of key groups that cover block i (i / 2 + 1), then
 //     dQ_i = scale * sum_{j<=i} dS_ij K_j on v_mfma_f32_32x32x2_f32, the i + 1
@@ -561,13 +566,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
             item = r * n_cu + c;
         }
         const int J = item / BHc, bhl = item % BHc;
-        // Wave priority by lightness: the arbiter otherwise favours the older
-        // (heavier, dispatched first) items, so that every key group finished
-        // its dK/dV item at about the same time and the dQ items ran after
-        // all of them (a timestamp trace at B=16 T=256: dK/dV items ending at
-        // 34-40 us, dQ items from 37 to 58 us). Light key groups first lets
-        // them reach their dQ items while the heavy ones are still running
-        // (12-layer step 1.0410 -> 1.0376 ms, A/B on one box).
+        // Wave priority by weight: the heaviest key groups (the longest chains
+        // of steps) issue first, so that their chains run at about a lone
+        // wave's speed while the lighter items fill the gaps (12-layer step,
+        // A/B on one box: heavy first 1.052 ms, no priorities 1.055 ms, light
+        // first 1.121 ms).
         {
             const int pr = n_kg - 1 - J;
             if (pr >= 3)
@@ -578,10 +581,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                 __builtin_amdgcn_s_setprio(1);
         }
         dkdv_item(J, bhl);
-        // the dQ blocks of this (b, h) that fall to key group J (see above)
+        // the dQ blocks of this (b, h) that fall to key group J: dealt by dQ
+        // work alone (see above)
         int load[kMaxFusedKeyGroups];
         for (int jg = 0; jg < n_kg; ++jg)
-            load[jg] = 8 * (n_qb - 2 * jg);
+            load[jg] = 0;
         uint32_t mine = 0;  // bit i: block i is this workgroup's
         for (int i = n_qb - 1; i >= 0; --i)
         {
