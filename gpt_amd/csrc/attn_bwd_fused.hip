@@ -22,19 +22,18 @@
 //     and one thread adds 1 to the completion counter of (b, h, i + 1); the
 //     last block's counter is bumped after a final wait.
 //   dQ items (b, h, query block i), done by the workgroups of the same
-//     (b, h) once their dK/dV item is done: the blocks are dealt to the key
-//     groups by dQ work alone, longest-processing-time first (from the
-//     heaviest block down, each to the key group with the least dQ work so
-//     far), which every workgroup computes the same way, so no queue or atomic
-//     is involved and every key group takes about the same dQ work (at B=16
-//     T=256 key groups 0..3 take blocks {4, 3}, {5, 2}, {6, 1}, {7, 0}).
-//     Weighting the dK/dV work in as well (a step as 8 units, dQ_i as i + 1)
-//     gave all the dQ work to the two lightest key groups, which under the
-//     wave priorities below end their dK/dV items no earlier than the heavy
-//     ones, so half of the workgroups ran all the dQ work after everything
-//     else (12-layer step 1.0443 -> 1.0085 ms when it went, A/B on one box).
-//     A workgroup runs its dQ items from the
-//     highest block down: wait until the counter of (b, h, i) reaches the
+//     (b, h) once their dK/dV item is done: key group J forms dQ of its own
+//     diagonal blocks 2J + 1 and 2J. Those are the last blocks it walks, and
+//     the lower key groups reach them at about the same step count, so they
+//     are complete about when J's dK/dV item ends and the dQ work needs no
+//     waiting; the light key groups, which finish first, take the big
+//     blocks. dQ items run at the lowest wave priority, behind the dK/dV
+//     items still in flight. (12-layer step, A/B on one box: 1.006 ms with the
+//     blocks dealt to the key groups by dQ work alone and the dK/dV
+//     priorities kept, 1.001 ms diagonal blocks, 0.985 ms diagonal blocks at
+//     priority 0; dealing the blocks by dK/dV plus dQ work, which gave all of
+//     them to the two lightest key groups, 1.044 ms.)
+//     A dQ item waits until the counter of (b, h, i) reaches the
 //     number of key groups that cover block i (i / 2 + 1), then
 //     dQ_i = scale * sum_{j<=i} dS_ij K_j on v_mfma_f32_32x32x2_f32, the i + 1
 //     units split over the 4 waves in contiguous ranges and the partials added
@@ -65,8 +64,9 @@ namespace gpt_attn {
 
 namespace {
 
-// The fused kernel computes the D rows itself and assigns dQ blocks with a
-// per-key-group table: rows of at most 4 key groups (T <= 256).
+// The fused kernel computes the D rows itself, which pays only up to T = 256
+// (at most 4 key groups; beyond it the two-launch form and a separate D-row
+// pass measure as fast or faster).
 constexpr int kMaxFusedKeyGroups = 4;
 
 // Spin limit of a dQ item waiting for its dS tiles (each spin sleeps about
@@ -581,29 +581,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                 __builtin_amdgcn_s_setprio(1);
         }
         dkdv_item(J, bhl);
-        // the dQ blocks of this (b, h) that fall to key group J: dealt by dQ
-        // work alone (see above)
-        int load[kMaxFusedKeyGroups];
-        for (int jg = 0; jg < n_kg; ++jg)
-            load[jg] = 0;
-        uint32_t mine = 0;  // bit i: block i is this workgroup's
-        for (int i = n_qb - 1; i >= 0; --i)
+        // dQ of this key group's own diagonal blocks (2J + 1, then 2J), at
+        // the lowest priority (see above)
+        __builtin_amdgcn_s_setprio(0);
+        for (int i = min(2 * J + 1, n_qb - 1); i >= 2 * J; --i)
         {
-            int best = n_kg - 1;
-            for (int jg = n_kg - 2; jg >= 0; --jg)
-                if (load[jg] < load[best])
-                    best = jg;
-            load[best] += i + 1;
-            if (best == J)
-                mine |= 1u << i;
-        }
-        for (int i = n_qb - 1; i >= 0; --i)
-        {
-            if (mine >> i & 1u)
-            {
-                __syncthreads();  // the previous item's LDS is free
-                dq_item(i, bhl);
-            }
+            __syncthreads();  // the previous item's LDS is free
+            dq_item(i, bhl);
         }
     }
 }
