@@ -22,10 +22,9 @@ import os
 
 import numpy as np
 
-from .pyoracle import REF_FAST_SO, REF_SO, _load
+from .pyoracle import LIBDIR, REF_FAST_SO, REF_SO, _load
 
-_HERE = os.path.dirname(os.path.abspath(__file__))
-OPS_SO = os.path.join(_HERE, "liboracle_ops.so")
+OPS_SO = os.path.join(LIBDIR, "liboracle_ops.so")
 
 _NAMES = {
     "embedding_forward": "embedding_forward",

@@ -23,9 +23,12 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-ORACLE_SO = os.path.join(_HERE, "liboracle_attn.so")
-REF_SO = os.path.join(_HERE, "_ref", "libref_cpu_attn.so")
-REF_FAST_SO = os.path.join(_HERE, "_ref", "libref_cpu_attn_fast.so")
+# GPT_ORACLE_LIBDIR selects another build of the same libraries, e.g.
+# oracle/_san (make -C oracle sanitize: AddressSanitizer + UBSan)
+LIBDIR = os.environ.get("GPT_ORACLE_LIBDIR", _HERE)
+ORACLE_SO = os.path.join(LIBDIR, "liboracle_attn.so")
+REF_SO = os.path.join(LIBDIR, "_ref", "libref_cpu_attn.so")
+REF_FAST_SO = os.path.join(LIBDIR, "_ref", "libref_cpu_attn_fast.so")
 
 _libs: dict = {}
 
