@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "attn_addr.h"
+
 namespace gpt_attn {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -165,12 +167,10 @@ __device__ __forceinline__ void wave_lds_sync()
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes)
 {
-    // (readfirstlane is int -> int: each half goes back through uint32_t, so
-    // that the low word is zero-extended, not sign-extended into the high word)
+    // (readfirstlane is int -> int; join_words zero-extends the low word)
     const uint64_t a = reinterpret_cast<uint64_t>(base);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-    const uint64_t u = ((uint64_t)hi << 32) | (uint64_t)lo;
+    const uint64_t u = join_words(__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)),
+                                  __builtin_amdgcn_readfirstlane((int)(uint32_t)a));
     return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(u), (short)0,
                                              __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000);
 }
