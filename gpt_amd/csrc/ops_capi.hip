@@ -188,10 +188,16 @@ int ws_get(const char *op, float **out, size_t floats, hipStream_t st, int slot 
 // use_lt would send to rocBLAS go to hipBLASLt only on a table hit.
 struct LtTuned
 {
+    int ver;  // hipBLASLt build (hipblasLtGetVersion) whose kernel this is
     bool ta, tb;
     int M, N, K, epi;
     unsigned long long kernel;  // FNV-1a 64 of the kernel name
 };
+// The two builds, by hipblasLtGetVersion: ROCm 7.2's (1.2.1) and PyTorch
+// 2.10+rocm7.0's bundled one (1.0.0). Any other build never reaches the
+// table (nor hipblaslt_ext, a C++ API whose types may differ between builds):
+// it takes the heuristic's first choice.
+constexpr int kLtRocm72 = 100201, kLtTorch = 100000;
 constexpr LtTuned kLtTuned[] = {
     // ROCm 7.2 build. Forward with the bias epilogue: qkv (MT192x64x16,
     // 126 -> 108 us; rocBLAS 122.5 + the bias pass), attention projection
@@ -199,49 +205,49 @@ constexpr LtTuned kLtTuned[] = {
     // stays on rocBLAS + the bias and GELU pass: its best bias-epilogue
     // kernel here (137.6 us + a GELU pass) would save about 10 us, but an
     // entry for it made the same call 15 us slower under PyTorch's build.
-    {false, false, 4096, 2304, 768, 1, 0xf3e165f544abc1d0ull},
-    {false, false, 4096, 768, 768, 1, 0xfc2ab4e5816e54c1ull},
-    {false, false, 4096, 768, 3072, 1, 0x97d87630ed7dfec3ull},
+    {kLtRocm72, false, false, 4096, 2304, 768, 1, 0xf3e165f544abc1d0ull},
+    {kLtRocm72, false, false, 4096, 768, 768, 1, 0xfc2ab4e5816e54c1ull},
+    {kLtRocm72, false, false, 4096, 768, 3072, 1, 0x97d87630ed7dfec3ull},
     // grad_x: qkv (MT192x32x32, 122 -> 109.5 us), attention projection
     // (MT128x32x32, 46 -> 43), FFN up (MT96x128x32, 143.5 -> 136.4), FFN down
     // (MT128x128x16, 139; rocBLAS 153.5)
-    {false, true, 4096, 768, 2304, 0, 0x6e3323c1c0733693ull},
-    {false, true, 4096, 768, 768, 0, 0x64e42940d84ef6b5ull},
-    {false, true, 4096, 768, 3072, 0, 0xf1575e4eba18b982ull},
-    {false, true, 4096, 3072, 768, 0, 0x00a8af8e17cf3704ull},
+    {kLtRocm72, false, true, 4096, 768, 2304, 0, 0x6e3323c1c0733693ull},
+    {kLtRocm72, false, true, 4096, 768, 768, 0, 0x64e42940d84ef6b5ull},
+    {kLtRocm72, false, true, 4096, 768, 3072, 0, 0xf1575e4eba18b982ull},
+    {kLtRocm72, false, true, 4096, 3072, 768, 0, 0x00a8af8e17cf3704ull},
     // grad_w: qkv (MT32x256x32, 138.7 -> 131 us), attention projection
     // (MT96x32x128, 133.7 -> 58.8); FFN up and down keep the first choice
-    {true, false, 768, 2304, 4096, 0, 0x966ae45d717321c0ull},
-    {true, false, 768, 768, 4096, 0, 0x262605300ea95f49ull},
+    {kLtRocm72, true, false, 768, 2304, 4096, 0, 0x966ae45d717321c0ull},
+    {kLtRocm72, true, false, 768, 768, 4096, 0, 0x262605300ea95f49ull},
     // PyTorch's bundled build. Forward: qkv (MT144x256x32, 150 -> 116 us;
     // rocBLAS 123 + the bias pass), attention projection (MT192x64x32,
     // 55-70 -> 47.5), FFN down (MT96x128x32, 154 -> 142); FFN up stays on
     // rocBLAS (142 + the bias and GELU pass against 147 + the GELU pass)
-    {false, false, 4096, 2304, 768, 1, 0x8c64e1e46bcba5cbull},
-    {false, false, 4096, 768, 768, 1, 0x9dbc1e588c20de9dull},
-    {false, false, 4096, 768, 3072, 1, 0xd72dbb1ca0f664ddull},
+    {kLtTorch, false, false, 4096, 2304, 768, 1, 0x8c64e1e46bcba5cbull},
+    {kLtTorch, false, false, 4096, 768, 768, 1, 0x9dbc1e588c20de9dull},
+    {kLtTorch, false, false, 4096, 768, 3072, 1, 0xd72dbb1ca0f664ddull},
     // grad_x: qkv (MT192x64x32, 135 -> 110.7 us), attention projection (the
     // same kernel, 51.9 -> 48), FFN up (MT96x128x32, 153 -> 141.5); FFN down
     // stays on rocBLAS (136 against 147)
-    {false, true, 4096, 768, 2304, 0, 0x5172d33dba3ee5f8ull},
-    {false, true, 4096, 768, 768, 0, 0x5172d33dba3ee5f8ull},
-    {false, true, 4096, 768, 3072, 0, 0x1410995819952b0eull},
+    {kLtTorch, false, true, 4096, 768, 2304, 0, 0x5172d33dba3ee5f8ull},
+    {kLtTorch, false, true, 4096, 768, 768, 0, 0x5172d33dba3ee5f8ull},
+    {kLtTorch, false, true, 4096, 768, 3072, 0, 0x1410995819952b0eull},
     // grad_w: qkv (MT32x256x32, 144 -> 130.5 us), attention projection
     // (MT32x96x64, 62.2 -> 60.9), FFN up and down (MT64x160x32, 168 -> 158,
     // 172-179 -> 156)
-    {true, false, 768, 2304, 4096, 0, 0xa8f15526ba86aa4eull},
-    {true, false, 768, 768, 4096, 0, 0xb66bfddbfc77941cull},
-    {true, false, 768, 3072, 4096, 0, 0x17a86e04fb1d2a39ull},
-    {true, false, 3072, 768, 4096, 0, 0x17a86e04fb1d2a39ull},
+    {kLtTorch, true, false, 768, 2304, 4096, 0, 0xa8f15526ba86aa4eull},
+    {kLtTorch, true, false, 768, 768, 4096, 0, 0xb66bfddbfc77941cull},
+    {kLtTorch, true, false, 768, 3072, 4096, 0, 0x17a86e04fb1d2a39ull},
+    {kLtTorch, true, false, 3072, 768, 4096, 0, 0x17a86e04fb1d2a39ull},
 };
 
 // Whether the table lists `kernel` for this GEMM (kernel 0: whether it lists
-// any kernel for it).
-bool lt_tuned(bool ta, bool tb, int M, int N, int K, int epi, unsigned long long kernel = 0)
+// any kernel for it) for hipBLASLt build `ver` (0: for any build).
+bool lt_tuned(bool ta, bool tb, int M, int N, int K, int epi, unsigned long long kernel = 0, int ver = 0)
 {
     for (const LtTuned &t : kLtTuned)
         if (t.ta == ta && t.tb == tb && t.M == M && t.N == N && t.K == K && t.epi == epi &&
-            (kernel == 0 || t.kernel == kernel))
+            (kernel == 0 || t.kernel == kernel) && (ver == 0 || t.ver == ver))
             return true;
     return false;
 }
@@ -289,6 +295,7 @@ struct LtPlan
 constexpr int kMaxPlans = 256;
 std::mutex g_lt_mu;
 hipblasLtHandle_t g_lt[kMaxDevices] = {};
+int g_lt_ver[kMaxDevices] = {};  // hipblasLtGetVersion of the loaded build (-1: unknown)
 LtPlan g_plans[kMaxPlans];
 int g_nplans = 0;
 
@@ -306,10 +313,15 @@ LtPlan *lt_plan(int dev, bool ta, bool tb, int M, int N, int K, int lda, int ldb
     }
     if (g_nplans == kMaxPlans || dev < 0 || dev >= kMaxDevices)
         return nullptr;
-    if (!g_lt[dev] && hipblasLtCreate(&g_lt[dev]) != HIPBLAS_STATUS_SUCCESS)
+    if (!g_lt[dev])
     {
-        g_lt[dev] = nullptr;
-        return nullptr;
+        if (hipblasLtCreate(&g_lt[dev]) != HIPBLAS_STATUS_SUCCESS)
+        {
+            g_lt[dev] = nullptr;
+            return nullptr;
+        }
+        int v = 0;
+        g_lt_ver[dev] = hipblasLtGetVersion(g_lt[dev], &v) == HIPBLAS_STATUS_SUCCESS && v > 0 ? v : -1;
     }
     LtPlan &q = g_plans[g_nplans++];
     q = LtPlan{dev, ta, tb, M, N, K, lda, ldb, ldc, epi, false, false, nullptr, nullptr, nullptr, nullptr, {}, 0};
@@ -350,7 +362,9 @@ LtPlan *lt_plan(int dev, bool ta, bool tb, int M, int N, int K, int lda, int ldb
     hipblasLtMatmulPreferenceDestroy(pref);
     if (!asked)
         return nullptr;
-    const bool listed = lt_tuned(ta, tb, M, N, K, epi);
+    // the table (and the kernel-name query) only for the two known builds
+    const int ver = g_lt_ver[dev];
+    const bool listed = (ver == kLtRocm72 || ver == kLtTorch) && lt_tuned(ta, tb, M, N, K, epi, 0, ver);
     int pick = -1;
     for (int i = 0; i < n; ++i)
     {
@@ -359,7 +373,8 @@ LtPlan *lt_plan(int dev, bool ta, bool tb, int M, int N, int K, int lda, int ldb
         if (pick < 0)
             pick = i;  // the heuristic's first workspace-free choice
         if (listed &&
-            lt_tuned(ta, tb, M, N, K, epi, fnv1a64(hipblaslt_ext::getKernelNameFromAlgo(g_lt[dev], res[i].algo))))
+            lt_tuned(ta, tb, M, N, K, epi, fnv1a64(hipblaslt_ext::getKernelNameFromAlgo(g_lt[dev], res[i].algo)),
+                     ver))
         {
             pick = i;
             q.tuned = true;
