@@ -17,6 +17,7 @@ from .attention import (  # noqa: F401
     device_ok,
     lib_path,
     load_library,
+    release_workspaces,
     set_path,
     timing_enable,
     timing_read,

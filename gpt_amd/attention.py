@@ -61,6 +61,8 @@ def load_library():
         lib.gpt_hip_attn_last_error.restype = ctypes.c_char_p
         lib.gpt_hip_attn_device_ok.argtypes = []
         lib.gpt_hip_attn_device_ok.restype = i
+        lib.gpt_hip_attn_release_workspaces.argtypes = []
+        lib.gpt_hip_attn_release_workspaces.restype = i
         lib.gpt_hip_attn_set_path.argtypes = [i]
         lib.gpt_hip_attn_set_path.restype = i
         lib.gpt_hip_attn_timing_enable.argtypes = [i]
@@ -181,6 +183,12 @@ def timing_read() -> dict:
     if rc < 0:
         _check(rc)
     return {k: (ms[i], cnt[i]) for i, k in enumerate(KERNEL_KINDS)}
+
+
+def release_workspaces() -> None:
+    """Frees the backward's per-stream dS workspaces on the current device
+    after waiting for its queued work; the next backward call allocates again."""
+    _check(load_library().gpt_hip_attn_release_workspaces())
 
 
 def set_path(path: int) -> int:

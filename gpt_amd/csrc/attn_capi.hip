@@ -165,6 +165,36 @@ hipError_t workspace_get(void **out, size_t bytes, hipStream_t st)
     return hipSuccess;
 }
 
+// Frees the workspaces of the current device once all its queued work is done.
+hipError_t workspace_release_device()
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return e;
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    e = hipDeviceSynchronize();
+    if (e != hipSuccess)
+        return e;
+    int n = 0;
+    for (int i = 0; i < g_ws_n; ++i)
+    {
+        if (g_ws[i].dev == dev)
+        {
+            if (g_ws[i].p)
+            {
+                const hipError_t f = hipFree(g_ws[i].p);
+                if (f != hipSuccess && e == hipSuccess)
+                    e = f;
+            }
+            continue;
+        }
+        g_ws[n++] = g_ws[i];
+    }
+    g_ws_n = n;
+    return e;
+}
+
 // Scratch of the no-allocation backward (gpt_hip_attn_bwd_f32_noalloc): a
 // fixed device array that holds the dS tiles in place of the per-stream
 // workspace. Each device the library runs on has its own copy, allocated when
@@ -423,6 +453,17 @@ int gpt_hip_attn_device_ok(void)
 {
     int n = 0;
     return hipGetDeviceCount(&n) == hipSuccess && n > 0 ? 1 : 0;
+}
+
+int gpt_hip_attn_release_workspaces(void)
+{
+    static const char *op = "gpt_hip_attn_release_workspaces";
+    if (int rc = check_device(op))
+        return rc;
+    const hipError_t e = workspace_release_device();
+    if (e != hipSuccess)
+        return fail(GPT_HIP_ATTN_ELAUNCH, "%s: %s", op, hipGetErrorString(e));
+    return 0;
 }
 
 int gpt_hip_attn_set_path(int path)

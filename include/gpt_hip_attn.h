@@ -97,6 +97,19 @@ int gpt_hip_attn_bwd_f32_noalloc(float *grad_x, float *D_cache, const float *lse
                                  int batch_size, int seq_len, int hidden_size, int num_heads,
                                  void *stream);
 
+/* Frees the default backward's dS workspaces on the calling thread's current
+ * device. gpt_hip_attn_bwd_f32 keeps one grow-only workspace per (device,
+ * stream) that it first ran on (up to 64 of them per process), so that calls
+ * allocate nothing after the first. This call waits for all work queued on
+ * the device (hipDeviceSynchronize), frees every workspace there and forgets
+ * its stream; the next backward call on a stream allocates again. For
+ * long-lived processes that retire streams or want the memory back. Backward
+ * calls on other host threads must not overlap it. Returns 0, or
+ * GPT_HIP_ATTN_ENODEV / GPT_HIP_ATTN_ELAUNCH with the HIP error in
+ * gpt_hip_attn_last_error(). No reference counterpart (the reference
+ * backward allocates no memory of its own). */
+int gpt_hip_attn_release_workspaces(void);
+
 /* Message for the last non-zero return on the calling thread ("" if none).
  * No reference counterpart: the reference prints and aborts instead
  * (src/backend/cuda/utils/cuda_utils.cuh:21-34); adapters that keep that

@@ -86,6 +86,12 @@ def test_no_device_is_reported():
     assert ei.value.code == ENODEV
 
 
+def test_release_workspaces_without_device_is_an_error():
+    if gpt_amd.device_ok():
+        pytest.skip("a HIP device is present")
+    assert gpt_amd.load_library().gpt_hip_attn_release_workspaces() == ENODEV
+
+
 def test_set_path_roundtrip():
     assert gpt_amd.set_path(1) == 0
     assert gpt_amd.set_path(0) == 1

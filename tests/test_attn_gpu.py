@@ -437,6 +437,27 @@ def test_backward_overwrites_grad_x_and_is_repeatable(dev):
         assert rel_err(gx[..., sl].cpu().numpy(), first[..., sl].cpu().numpy()) <= 1e-6
 
 
+@pytest.mark.parametrize("T", [256, 300])
+def test_release_workspaces_then_backward_again(dev, T):
+    """gpt_hip_attn_release_workspaces frees the per-stream dS workspace; the
+    next backward allocates a new one (its control block zeroed again) and
+    gives the same bits, on the fused (T <= 256) and the two-launch form.
+    Releasing with nothing allocated is a no-op."""
+    import torch
+
+    B, C, H = 3, 768, 12
+    x = _to(dev, synth.qkv(B, T, C, 500 + T))
+    g = _to(dev, synth.grad_out(B, T, C, 500 + T))
+    y, lse = gpt_amd.attention_forward(x, H)
+    first, D0 = gpt_amd.attention_backward(x, y, lse, g, H)
+    gpt_amd.release_workspaces()
+    gpt_amd.release_workspaces()
+    again, D1 = gpt_amd.attention_backward(x, y, lse, g, H)
+    torch.cuda.synchronize()
+    assert torch.isfinite(first).all()
+    assert torch.equal(first, again) and torch.equal(D0, D1)
+
+
 def test_inputs_untouched_and_side_stream(dev):
     import torch
 
