@@ -754,6 +754,7 @@ def main():
             gpt_amd.device_flash_attention_backward(gx[layer], Dc[layer], lse[layer], dout[layer], y[layer],
                                                     qkv[layer], B, T, C, H, stream)
 
+    gpt_amd.wait_timeouts()  # clear counts left by earlier work in this process
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -779,6 +780,11 @@ def main():
     torch.cuda.synchronize()
     per_kernel = gpt_amd.timing_read()
     gpt_amd.timing_enable(False)
+    # A dQ wait that gave up at its spin limit computed from incomplete dS
+    # tiles: the measured work would not be the op's, so the run fails.
+    timeouts = gpt_amd.wait_timeouts()
+    if timeouts:
+        sys.exit(f"bench.py: {timeouts} dQ waits of the one-launch backward hit their spin limit")
 
     ms_per_step = total_ms / args.steps
     step_flops = LAYERS * attn_flops(B, T, H, D_HEAD)

@@ -21,4 +21,5 @@ from .attention import (  # noqa: F401
     set_path,
     timing_enable,
     timing_read,
+    wait_timeouts,
 )

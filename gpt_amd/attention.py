@@ -61,6 +61,8 @@ def load_library():
         lib.gpt_hip_attn_last_error.restype = ctypes.c_char_p
         lib.gpt_hip_attn_device_ok.argtypes = []
         lib.gpt_hip_attn_device_ok.restype = i
+        lib.gpt_hip_attn_wait_timeouts.argtypes = []
+        lib.gpt_hip_attn_wait_timeouts.restype = i
         lib.gpt_hip_attn_release_workspaces.argtypes = []
         lib.gpt_hip_attn_release_workspaces.restype = i
         lib.gpt_hip_attn_set_path.argtypes = [i]
@@ -183,6 +185,16 @@ def timing_read() -> dict:
     if rc < 0:
         _check(rc)
     return {k: (ms[i], cnt[i]) for i, k in enumerate(KERNEL_KINDS)}
+
+
+def wait_timeouts() -> int:
+    """Waits for the device, then returns (and clears) how many dQ waits of
+    the one-launch backward hit their spin limit since the last call (0 in
+    every correct run)."""
+    rc = load_library().gpt_hip_attn_wait_timeouts()
+    if rc < 0:
+        _check(rc)
+    return rc
 
 
 def release_workspaces() -> None:

@@ -485,7 +485,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                 if (++spins >= kTileSpinLimit)
                 {
                     if (lane == 0)
-                        __hip_atomic_fetch_add(ctl + 16, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_fetch_add(ctl + kCtlWaitErrors, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;
                 }
             }

@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <climits>
 #include <mutex>
 #include <stdarg.h>
 #include <stdint.h>
@@ -453,6 +454,42 @@ int gpt_hip_attn_device_ok(void)
 {
     int n = 0;
     return hipGetDeviceCount(&n) == hipSuccess && n > 0 ? 1 : 0;
+}
+
+int gpt_hip_attn_wait_timeouts(void)
+{
+    static const char *op = "gpt_hip_attn_wait_timeouts";
+    if (int rc = check_device(op))
+        return rc;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    // every control block of this device: the per-stream workspaces and, once
+    // looked up, the no-allocation entry point's scratch array
+    int *blocks[kMaxWorkspaces + 1];
+    int n = 0;
+    {
+        std::lock_guard<std::mutex> lock(g_ws_mu);
+        for (int i = 0; i < g_ws_n && e == hipSuccess; ++i)
+            if (g_ws[i].dev == dev && g_ws[i].p)
+                blocks[n++] = static_cast<int *>(g_ws[i].p);
+    }
+    float *sp = nullptr;
+    if (e == hipSuccess && scratch_addr(&sp) == hipSuccess && sp)
+        blocks[n++] = reinterpret_cast<int *>(sp);
+    if (e == hipSuccess)
+        e = hipDeviceSynchronize();
+    long total = 0;
+    for (int i = 0; i < n && e == hipSuccess; ++i)
+    {
+        int v = 0;
+        e = hipMemcpy(&v, blocks[i] + gpt_attn::kCtlWaitErrors, sizeof(int), hipMemcpyDeviceToHost);
+        if (e == hipSuccess && v != 0)
+            e = hipMemset(blocks[i] + gpt_attn::kCtlWaitErrors, 0, sizeof(int));
+        total += v;
+    }
+    if (e != hipSuccess)
+        return fail(GPT_HIP_ATTN_ELAUNCH, "%s: %s", op, hipGetErrorString(e));
+    return total > INT_MAX ? INT_MAX : (int)total;
 }
 
 int gpt_hip_attn_release_workspaces(void)

@@ -78,6 +78,9 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
 // of the workspace, is zeroed when the workspace is allocated and is left
 // all zeros by every launch.
 constexpr size_t kCtlBytes = size_t(1) << 20;
+// Control-block word that counts the fused backward's dQ waits that hit
+// their spin limit.
+constexpr int kCtlWaitErrors = 16;
 size_t bwd_fused_ctl_ints(const Shape &s, int bh_per_chunk);
 
 // Backward, head_dim 64, fp32 MFMA, deterministic, one launch (plus the D-row

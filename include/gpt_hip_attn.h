@@ -97,6 +97,17 @@ int gpt_hip_attn_bwd_f32_noalloc(float *grad_x, float *D_cache, const float *lse
                                  int batch_size, int seq_len, int hidden_size, int num_heads,
                                  void *stream);
 
+/* Number of dQ waits in the one-launch backward (T <= 256) that gave up at
+ * their spin limit, on the calling thread's current device, since the last
+ * call; the counts are cleared. Waits for all work queued on the device
+ * first (hipDeviceSynchronize). A wait ends once the dK/dV work it waits for
+ * has stored its dS tiles, which every workgroup of the launch does without
+ * waiting itself, so any correct run returns 0; a nonzero count means that
+ * many dQ items read incomplete tiles (wrong dQ rows). Returns the count
+ * (>= 0), or GPT_HIP_ATTN_ENODEV / GPT_HIP_ATTN_ELAUNCH. No reference
+ * counterpart (the reference's dQ uses atomics and never waits). */
+int gpt_hip_attn_wait_timeouts(void);
+
 /* Frees the default backward's dS workspaces on the calling thread's current
  * device. gpt_hip_attn_bwd_f32 keeps one grow-only workspace per (device,
  * stream) that it first ran on (up to 64 of them per process), so that calls

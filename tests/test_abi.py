@@ -90,6 +90,7 @@ def test_release_workspaces_without_device_is_an_error():
     if gpt_amd.device_ok():
         pytest.skip("a HIP device is present")
     assert gpt_amd.load_library().gpt_hip_attn_release_workspaces() == ENODEV
+    assert gpt_amd.load_library().gpt_hip_attn_wait_timeouts() == ENODEV
 
 
 def test_set_path_roundtrip():

@@ -25,6 +25,15 @@ from tests.tolerances import BWD_RTOL, ELEM_ATOL_FRAC, FWD_RTOL, assert_close, r
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def no_wait_timeouts(dev):
+    """After every test: no dQ wait of the one-launch backward gave up at its
+    spin limit (each would have read incomplete dS tiles)."""
+    gpt_amd.wait_timeouts()
+    yield
+    assert gpt_amd.wait_timeouts() == 0
+
+
 def _to(dev, a):
     import torch
 

@@ -14,6 +14,14 @@ from gpt_amd import synth
 
 pytestmark = pytest.mark.gpu
 
+
+@pytest.fixture(autouse=True)
+def no_wait_timeouts(dev):
+    """The scratch array's control block records no timed-out dQ wait."""
+    gpt_amd.wait_timeouts()
+    yield
+    assert gpt_amd.wait_timeouts() == 0
+
 ERANGE = -6
 
 
