@@ -175,6 +175,36 @@ def test_config5b_prefix_sweep_T1_to_256(dev):
     print("C5b worst O/LSE rel err", worst)
 
 
+def test_backward_sweep_T1_to_256(dev):
+    """Backward at B=1 (12 heads) for every T = 1..256 against the oracle: every
+    query-block count and ragged tail of the one-launch backward (1 to 4 key
+    groups, odd and even block counts, rows past T in the last block), with
+    one workspace growing call by call; the two-launch form (path 3) on every
+    fifth T. Inputs are the prefixes of one B=1, T=256 draw, as generation
+    would see them; dO is drawn at unit scale so that every row matters."""
+    C, H = 768, 12
+    x = synth.qkv(1, 256, C, seed=1240)
+    g = synth.grad_out(1, 256, C, seed=1240, std=1.0)
+    worst = {}
+    for T in range(1, 257):
+        xt, gt = np.ascontiguousarray(x[:, :T]), np.ascontiguousarray(g[:, :T])
+        yr, lr = pyoracle.forward(xt, H)
+        gr, Dr = pyoracle.backward(xt, yr, lr, gt, H)
+        paths = (0, 3) if T % 5 == 0 else (0,)
+        for path in paths:
+            prev = gpt_amd.set_path(path)
+            try:
+                gx, D = gpu_bwd(dev, xt, yr, lr, gt, H)
+            finally:
+                gpt_amd.set_path(prev)
+            for name, a, r in (("dQ", gx[..., :C], gr[..., :C]), ("dK", gx[..., C:2 * C], gr[..., C:2 * C]),
+                               ("dV", gx[..., 2 * C:], gr[..., 2 * C:]), ("D", D, Dr)):
+                e = rel_err(a, r)
+                assert e <= BWD_RTOL, (T, path, name, e)
+                worst[name] = max(worst.get(name, 0.0), e)
+    print("backward sweep T=1..256 worst rel err", worst)
+
+
 @pytest.mark.parametrize("B,T,C,H", [(1, 64, 32, 4), (2, 50, 64, 4), (1, 40, 60, 4), (1, 33, 96, 3),
                                      (1, 70, 256, 2), (2, 17, 24, 3)])
 def test_general_head_dim(dev, B, T, C, H):
