@@ -465,14 +465,13 @@ int gpt_hip_attn_wait_timeouts(void)
     hipError_t e = hipGetDevice(&dev);
     // every control block of this device: the per-stream workspaces and, once
     // looked up, the no-allocation entry point's scratch array
+    // (the lock is held throughout, so that no workspace is freed meanwhile)
+    std::lock_guard<std::mutex> lock(g_ws_mu);
     int *blocks[kMaxWorkspaces + 1];
     int n = 0;
-    {
-        std::lock_guard<std::mutex> lock(g_ws_mu);
-        for (int i = 0; i < g_ws_n && e == hipSuccess; ++i)
-            if (g_ws[i].dev == dev && g_ws[i].p)
-                blocks[n++] = static_cast<int *>(g_ws[i].p);
-    }
+    for (int i = 0; i < g_ws_n && e == hipSuccess; ++i)
+        if (g_ws[i].dev == dev && g_ws[i].p)
+            blocks[n++] = static_cast<int *>(g_ws[i].p);
     float *sp = nullptr;
     if (e == hipSuccess && scratch_addr(&sp) == hipSuccess && sp)
         blocks[n++] = reinterpret_cast<int *>(sp);
