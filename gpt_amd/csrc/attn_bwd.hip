@@ -510,9 +510,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
         if (key < T)
         {
             float *dst = gx + (long)key * 3 * C + 4 * c16;
-            *reinterpret_cast<float4 *>(dst + C) =
-                make_float4(dk0[r] * scale, dk1[r] * scale, dk2[r] * scale, dk3[r] * scale);
-            *reinterpret_cast<float4 *>(dst + 2 * C) = make_float4(dv0[r], dv1[r], dv2[r], dv3[r]);
+            store4_nt(dst + C, make_float4(dk0[r] * scale, dk1[r] * scale, dk2[r] * scale, dk3[r] * scale));
+            store4_nt(dst + 2 * C, make_float4(dv0[r], dv1[r], dv2[r], dv3[r]));
         }
     }
 }
@@ -649,8 +648,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                 s.w += x.w;
             }
             if (row < T)
-                *reinterpret_cast<float4 *>(gx + (long)row * 3 * C + 4 * (e & 15)) =
-                    make_float4(s.x * scale, s.y * scale, s.z * scale, s.w * scale);
+                store4_nt(gx + (long)row * 3 * C + 4 * (e & 15),
+                          make_float4(s.x * scale, s.y * scale, s.z * scale, s.w * scale));
         }
     };
 
