@@ -322,6 +322,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
         const int q0 = 32 * i;
         const auto Bf = bufs(buf_c);
         const float *Qs = Bf.q, *Os = Bf.o, *LDs = Bf.ld;
+        // (dS tiles with the non-temporal hint: the dQ kernel reads each once;
+        // C4 -0.5 %, C5a -0.9 %, while non-temporal loads of them in the dQ
+        // kernel measured 5 % slower)
         float *tile = ws + ds_tile(i, kw0 >> 5) + (kw0 & 31) + c16 + (4 * g4) * 32;
         // Half t of the tile: queries q0 + 16 t .. + 15 against this wave's
         // 16 keys, done start to end (S, dP, P, dS, its dS rows, dV and dK)
@@ -371,7 +374,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
             // this wave's 16 x 16 quarter of dS tile (i, kw0 / 32), query-major
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                tile[(16 * t + r) * 32] = pa[r];
+                __builtin_nontemporal_store(pa[r], &tile[(16 * t + r) * 32]);
             // dV += P^T dO, dK += dS^T Q: step r contracts queries
             // q0 + 16t + 4kk + r (kk = l/16); B operands dO / Q[that query][4 c16 + e]
 #pragma unroll
@@ -402,7 +405,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                 {
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        tile[r * 32] = 0.f;
+                        __builtin_nontemporal_store(0.f, &tile[r * 32]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 half(BufIdx<1>{});
@@ -457,8 +460,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
 #pragma unroll
             for (int r = 0; r < 4; ++r)
             {
-                tile[r * 32] = p0[r];
-                tile[(16 + r) * 32] = p1[r];
+                __builtin_nontemporal_store(p0[r], &tile[r * 32]);
+                __builtin_nontemporal_store(p1[r], &tile[(16 + r) * 32]);
             }
 #pragma unroll
             for (int t = 0; t < 2; ++t)
