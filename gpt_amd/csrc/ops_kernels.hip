@@ -806,7 +806,12 @@ __global__ __launch_bounds__(256) void ce_bwd_kernel(float *__restrict__ gx, con
         float *dst = gx + r * Vp + c;
         if (c + 3 < V)
         {
-            *reinterpret_cast<float4 *>(dst) = o;
+            // non-temporal: the 824 MB of logit gradients of a GPT-2 step
+            // stream out without taking cache lines (341 -> 272 us per call;
+            // the hint on softmax's and AdamW's outputs changed nothing)
+            typedef float f4v __attribute__((ext_vector_type(4)));
+            const f4v ov = {o.x, o.y, o.z, o.w};
+            __builtin_nontemporal_store(ov, reinterpret_cast<f4v *>(dst));
         }
         else
         {
