@@ -224,10 +224,12 @@ __device__ __forceinline__ void vm_wait()
 }
 __device__ __forceinline__ void lds_dma_wait() { vm_wait<0>(); }
 
-// Workgroup barrier that orders LDS only: unlike __syncthreads(), whose
-// fences also cover global memory and so wait for every outstanding global
-// store (vmcnt(0)), it waits for this wave's LDS operations alone. Loads to
-// LDS count in vmcnt and must be waited for (vm_wait) before it.
+// Workgroup barrier that orders LDS only: it waits for this wave's LDS
+// operations alone. On gfx950 outside thread-group split mode
+// __syncthreads() compiles to the same code (its workgroup-scope fences need
+// no vmcnt wait there, so neither waits for outstanding global stores); this
+// form states the intent. Loads to LDS count in vmcnt and must be waited for
+// (vm_wait) before it.
 __device__ __forceinline__ void lds_barrier()
 {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
