@@ -90,7 +90,7 @@ __device__ __forceinline__ int load_agent(const int *p)
 
 }  // namespace
 
-template <bool FUSE_D>
+template <bool FUSE_D, bool HELP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void bwd_fused_d64_kernel(
     float *__restrict__ grad_x, float *__restrict__ dsw, int *__restrict__ ctl, const float *__restrict__ lse,
     float *__restrict__ Dv, const float *__restrict__ dy, const float *__restrict__ y, const float *__restrict__ qkv,
@@ -240,15 +240,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
         int done_prev = -1;  // block whose dS stores the next barrier covers
         // One query block. GEN: a diagonal block (i = 2J, 2J + 1), which tests
         // for skipped tiles and zero halves and applies the causal mask.
+        // Keys whose units a wave computes in a diagonal step, and halves it
+        // leaves out: in the last step (block 2J) wave 2 takes wave 0's
+        // second half (see below); otherwise every wave computes its own keys.
+        int kwe_m = kw0;
+        bool skip0_m = false, skip1_m = false;
         auto step = [&](const int i, auto buf_c, auto gen_c) {
             constexpr int buf = decltype(buf_c)::value;
             constexpr bool GEN = decltype(gen_c)::value;
+            const int kwe = HELP ? kwe_m : kw0;
+            const bool skip0 = HELP && skip0_m, skip1 = HELP && skip1_m;
             issue(i - 1, BufIdx<buf ^ 1>{});
             __builtin_amdgcn_sched_barrier(0);
             const int q0 = 32 * i;
             const auto Bf = bufs(buf_c);
             const float *Qs = Bf.q, *Os = Bf.o, *LDs = Bf.ld;
-            float *tile = ws + ((long)i * (i + 1) / 2 + (kw0 >> 5)) * 1024 + (kw0 & 31) + c16 + (4 * g4) * 32;
+            float *tile = ws + ((long)i * (i + 1) / 2 + (kwe >> 5)) * 1024 + (kwe & 31) + c16 + (4 * g4) * 32;
             auto half = [&](auto t_c) {
                 constexpr int t = decltype(t_c)::value;
                 v4f sa = zero4(), pa = zero4();
@@ -278,9 +285,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                         sa[r] = p;
                         pa[r] = p * (pa[r] - dv[r]);
                     }
-                    if (GEN && q0 + 16 * t < kw0 + 15)
+                    if (GEN && q0 + 16 * t < kwe + 15)
                     {
-                        const int key = kw0 + c16;
+                        const int key = kwe + c16;
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
                             if (key > q0 + 16 * t + 4 * g4 + r)
@@ -308,10 +315,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
             };
             if constexpr (GEN)
             {
-                if (kw0 <= q0 + 31)
+                if (kwe <= q0 + 31)
                 {
-                    if (kw0 < q0 + 16)
-                        half(BufIdx<0>{});
+                    if (kwe < q0 + 16)
+                    {
+                        if (!skip0)
+                            half(BufIdx<0>{});
+                    }
                     else
                     {
 #pragma unroll
@@ -319,7 +329,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                             store_sc1(tile + r * 32, 0.f);
                     }
                     __builtin_amdgcn_sched_barrier(0);
-                    half(BufIdx<1>{});
+                    if (!skip1)
+                        half(BufIdx<1>{});
                     __builtin_amdgcn_sched_barrier(0);
                     vm_wait<8>();
                 }
@@ -415,22 +426,108 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
         }
         if (i_lo + 1 < n_qb)
             step(i_lo + 1, BufIdx<1>{}, BufIdx<1>{});
-        step(i_lo, BufIdx<0>{}, BufIdx<1>{});
-        lds_dma_wait();
-        lds_barrier();
-        if (tid == 0)
-            __hip_atomic_fetch_add(cnt_bh + done_prev, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
-        // register r of lane l: key kw0 + 4 g4 + r, dims 4 c16 + e
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
+        if constexpr (HELP)
         {
-            const int key = kw0 + 4 * g4 + r;
-            if (key < T)
+            // register r of lane l: key kw0 + 4 g4 + r, dims 4 c16 + e
+            auto store_rows = [&]() {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                {
+                    const int key = kw0 + 4 * g4 + r;
+                    if (key < T)
+                    {
+                        float *dst = gx_out + (long)key * 3 * C + 4 * c16;
+                        store4_nt(dst + C, make_float4(dk0[r] * scale, dk1[r] * scale, dk2[r] * scale, dk3[r] * scale));
+                        store4_nt(dst + 2 * C, make_float4(dv0[r], dv1[r], dv2[r], dv3[r]));
+                    }
+                }
+            };
+            // Last step (block 2J, queries 64J .. 64J + 31): wave 0 (keys 64J ..
+            // + 15) has two halves of work, wave 1 one, waves 2 and 3 (keys past
+            // the block's queries) none. With HELP (the launcher takes it for
+            // grids of at most 2 workgroups per CU, where no other workgroup's
+            // waves fill that idle time), wave 2, whose keys are finished, stores
+            // them, takes wave 0's K and V rows and computes wave 0's second half
+            // from zero; wave 0 adds that partial after the step. (Step at B=8
+            // T=256, 12 layers: 0.6684 vs 0.6762 ms; on full grids the same code
+            // lost 0.6 % at C3 even switched off, so it is an instantiation of
+            // its own.)
+                if (w == 2)
             {
-                float *dst = gx_out + (long)key * 3 * C + 4 * c16;
-                store4_nt(dst + C, make_float4(dk0[r] * scale, dk1[r] * scale, dk2[r] * scale, dk3[r] * scale));
-                store4_nt(dst + 2 * C, make_float4(dv0[r], dv1[r], dv2[r], dv3[r]));
+                store_rows();
+                const uint32_t off = (uint32_t)c16 * Wb + 64u * g4;
+                kwe_m = kw0 - 32;
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                {
+                    const float4 k4 = bload4s(rq, off + Cb + 16u * c, (uint32_t)kwe_m * Wb);
+                    const float4 v4 = bload4s(rq, off + 2u * Cb + 16u * c, (uint32_t)kwe_m * Wb);
+                    kreg[4 * c + 0] = k4.x;
+                    kreg[4 * c + 1] = k4.y;
+                    kreg[4 * c + 2] = k4.z;
+                    kreg[4 * c + 3] = k4.w;
+                    vreg[4 * c + 0] = v4.x;
+                    vreg[4 * c + 1] = v4.y;
+                    vreg[4 * c + 2] = v4.z;
+                    vreg[4 * c + 3] = v4.w;
+                }
+                dk0 = dk1 = dk2 = dk3 = zero4();
+                dv0 = dv1 = dv2 = dv3 = zero4();
+                skip0_m = true;
+            }
+            else if (w == 0)
+                skip1_m = true;
+            step(i_lo, BufIdx<0>{}, BufIdx<1>{});
+            lds_dma_wait();
+            lds_barrier();
+            if (tid == 0)
+                __hip_atomic_fetch_add(cnt_bh + done_prev, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // wave 2's partial through buffer 1's Q tile (free: the last step
+            // read buffer 0, and every wave's staging loads have landed)
+            float4 *part = reinterpret_cast<float4 *>(sq1) + lane;
+            if (w == 2)
+            {
+                const v4f acc[8] = {dk0, dk1, dk2, dk3, dv0, dv1, dv2, dv3};
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    part[64 * k] = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+            }
+            lds_barrier();
+            if (w == 0)
+            {
+                v4f *acc[8] = {&dk0, &dk1, &dk2, &dk3, &dv0, &dv1, &dv2, &dv3};
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                {
+                    const float4 u = part[64 * k];
+                    (*acc[k])[0] += u.x;
+                    (*acc[k])[1] += u.y;
+                    (*acc[k])[2] += u.z;
+                    (*acc[k])[3] += u.w;
+                }
+            }
+            if (w != 2)
+                store_rows();
+        }
+        else
+        {
+            step(i_lo, BufIdx<0>{}, BufIdx<1>{});
+            lds_dma_wait();
+            lds_barrier();
+            if (tid == 0)
+                __hip_atomic_fetch_add(cnt_bh + done_prev, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+            // register r of lane l: key kw0 + 4 g4 + r, dims 4 c16 + e
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+            {
+                const int key = kw0 + 4 * g4 + r;
+                if (key < T)
+                {
+                    float *dst = gx_out + (long)key * 3 * C + 4 * c16;
+                    store4_nt(dst + C, make_float4(dk0[r] * scale, dk1[r] * scale, dk2[r] * scale, dk3[r] * scale));
+                    store4_nt(dst + 2 * C, make_float4(dv0[r], dv1[r], dv2[r], dv3[r]));
+                }
             }
         }
     };
@@ -649,9 +746,14 @@ hipError_t launch_bwd_fused_d64(float *grad_x, float *D, const float *lse, const
     const int BH = s.B * s.H;
     const float scale = 1.0f / sqrtf(64.f);
     const dim3 g((unsigned)(n_kg * BH));
-    // T <= 256 (bwd_fused_d64_fits): the D rows are computed in the kernel
-    launch_timed(kKindFused, bwd_fused_d64_kernel<true>, g, dim3(256), st, grad_x, ws, ctl, lse, D, dy, y, qkv, s.T,
-                 s.C, s.H, 0, BH, n_qb, scale * kLog2e, scale, n_cu);
+    // T <= 256 (bwd_fused_d64_fits): the D rows are computed in the kernel;
+    // grids of at most 2 workgroups per CU share the last step's work out
+    if (n_kg * BH <= 2 * n_cu)
+        launch_timed(kKindFused, bwd_fused_d64_kernel<true, true>, g, dim3(256), st, grad_x, ws, ctl, lse, D, dy, y,
+                     qkv, s.T, s.C, s.H, 0, BH, n_qb, scale * kLog2e, scale, n_cu);
+    else
+        launch_timed(kKindFused, bwd_fused_d64_kernel<true, false>, g, dim3(256), st, grad_x, ws, ctl, lse, D, dy, y,
+                     qkv, s.T, s.C, s.H, 0, BH, n_qb, scale * kLog2e, scale, n_cu);
     return hipGetLastError();
 }
 
