@@ -19,6 +19,7 @@ from .attention import (  # noqa: F401
     load_library,
     release_workspaces,
     set_path,
+    set_wait_limit,
     timing_enable,
     timing_read,
     wait_timeouts,

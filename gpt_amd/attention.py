@@ -67,6 +67,8 @@ def load_library():
         lib.gpt_hip_attn_release_workspaces.restype = i
         lib.gpt_hip_attn_set_path.argtypes = [i]
         lib.gpt_hip_attn_set_path.restype = i
+        lib.gpt_hip_attn_set_wait_limit.argtypes = [ctypes.c_longlong, i]
+        lib.gpt_hip_attn_set_wait_limit.restype = i
         lib.gpt_hip_attn_timing_enable.argtypes = [i]
         lib.gpt_hip_attn_timing_enable.restype = i
         lib.gpt_hip_attn_timing_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int), i]
@@ -189,12 +191,20 @@ def timing_read() -> dict:
 
 def wait_timeouts() -> int:
     """Waits for the device, then returns (and clears) how many dQ waits of
-    the one-launch backward hit their spin limit since the last call (0 in
-    every correct run)."""
+    the one-launch backward reached their time limit since the last call (0
+    in every correct run)."""
     rc = load_library().gpt_hip_attn_wait_timeouts()
     if rc < 0:
         _check(rc)
     return rc
+
+
+def set_wait_limit(microseconds: int = -1, extra_need: int = 0) -> None:
+    """Test hook for the one-launch backward's dQ waits: time limit of one
+    wait (negative = the default, one second) and a count added to every
+    awaited count (extra_need > 0 makes every such wait run to the limit).
+    Process-wide; read at each launch."""
+    _check(load_library().gpt_hip_attn_set_wait_limit(int(microseconds), int(extra_need)))
 
 
 def release_workspaces() -> None:

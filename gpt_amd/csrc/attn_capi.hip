@@ -28,6 +28,28 @@ thread_local char g_err[512] = "";
 // only, 2 atomic-dQ backward, 3 two-launch backward at every T; read once per
 // call
 std::atomic<int> g_path{0};
+// Time limit of the fused backward's dQ waits, in microseconds, and the test
+// hook's extra count (gpt_hip_attn_set_wait_limit).
+constexpr long long kDefaultWaitUs = 1000000;
+std::atomic<long long> g_wait_us{kDefaultWaitUs};
+std::atomic<int> g_need_extra{0};
+
+// Wall-clock ticks (wall_clock64) per microsecond of the current device.
+long long wall_ticks_per_us()
+{
+    static long long cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return 100;
+    if (cached[dev] == 0)
+    {
+        int khz = 0;
+        if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0)
+            khz = 100000;  // 100 MHz, the gfx9 real-time counter
+        cached[dev] = (khz + 999) / 1000;
+    }
+    return cached[dev];
+}
 
 
 int fail(int code, const char *fmt, ...)
@@ -113,13 +135,30 @@ struct Workspace
     hipStream_t st;
     void *p;
     size_t bytes;
+    unsigned epoch;  // of the last fused-backward launch on this control block
 };
 constexpr int kMaxWorkspaces = 64;
 std::mutex g_ws_mu;
 Workspace g_ws[kMaxWorkspaces];
 int g_ws_n = 0;
 
-hipError_t workspace_get(void **out, size_t bytes, hipStream_t st)
+// Next launch epoch of a control block: never 0 (the value of a zeroed
+// block), different from the previous one.
+unsigned next_epoch(unsigned e) { return e + 1 == 0 ? 1 : e + 1; }
+
+// Zeroes n ints (the control block of a new workspace). A kernel rather than
+// hipMemsetAsync, so that no memset node is ever recorded into a graph.
+__global__ void zero_ints_kernel(int *p, int n)
+{
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+// Device buffer of at least `bytes` bytes for the backward on `st`, and the
+// epoch for its next fused launch. Refuses (hipErrorStreamCaptureUnsupported)
+// to allocate while `st` is capturing a graph: such callers take
+// gpt_hip_attn_bwd_f32_noalloc, or make one call before capturing.
+hipError_t workspace_get(void **out, unsigned *epoch, size_t bytes, hipStream_t st)
 {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -135,10 +174,16 @@ hipError_t workspace_get(void **out, size_t bytes, hipStream_t st)
         if (g_ws_n == kMaxWorkspaces)
             return hipErrorOutOfMemory;
         w = &g_ws[g_ws_n++];
-        *w = Workspace{dev, st, nullptr, 0};
+        *w = Workspace{dev, st, nullptr, 0, 0};
     }
     if (w->bytes < bytes)
     {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(st, &cs);
+        if (e != hipSuccess)
+            return e;
+        if (cs != hipStreamCaptureStatusNone)
+            return hipErrorStreamCaptureUnsupported;
         if (w->p)
         {
             // the old buffer may still be read by work queued on this stream
@@ -152,7 +197,11 @@ hipError_t workspace_get(void **out, size_t bytes, hipStream_t st)
         }
         e = hipMalloc(&w->p, bytes);
         if (e == hipSuccess)  // the fused backward's control block starts out zeroed
-            e = hipMemsetAsync(w->p, 0, gpt_attn::kCtlBytes, st);
+        {
+            hipLaunchKernelGGL(zero_ints_kernel, dim3(256), dim3(256), 0, st, static_cast<int *>(w->p),
+                               (int)(gpt_attn::kCtlBytes / sizeof(int)));
+            e = hipGetLastError();
+        }
         if (e != hipSuccess)
         {
             if (w->p)
@@ -163,6 +212,8 @@ hipError_t workspace_get(void **out, size_t bytes, hipStream_t st)
         w->bytes = bytes;
     }
     *out = w->p;
+    w->epoch = next_epoch(w->epoch);
+    *epoch = w->epoch;
     return hipSuccess;
 }
 
@@ -211,12 +262,14 @@ struct ScratchAddr
     std::once_flag once;
     hipError_t err = hipSuccess;
     float *p = nullptr;
+    std::atomic<unsigned> epoch{0};  // of the last fused-backward launch on its control block
 };
 ScratchAddr g_scratch[kMaxDevices];
 
 // Device address of the current device's scratch array (looked up on the
-// first call per device, with that device current).
-hipError_t scratch_addr(float **out)
+// first call per device, with that device current) and, when `epoch` is
+// given, the epoch for the next fused launch on its control block.
+hipError_t scratch_addr(float **out, unsigned *epoch = nullptr)
 {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -233,6 +286,14 @@ hipError_t scratch_addr(float **out)
     if (s.err != hipSuccess)
         return s.err;
     *out = s.p;
+    if (epoch)
+    {
+        unsigned e = s.epoch.load(std::memory_order_relaxed), n;
+        do
+            n = next_epoch(e);
+        while (!s.epoch.compare_exchange_weak(e, n, std::memory_order_relaxed));
+        *epoch = n;
+    }
     return hipSuccess;
 }
 
@@ -314,12 +375,8 @@ int backward(const char *op, bool noalloc, float *grad_x, float *D_cache, const 
     int chunk = 0;
     const size_t bytes =
         gpt_attn::bwd_d64_workspace_bytes(s, noalloc ? kScratchBytes : gpt_attn::kWorkspaceCap, &chunk);
-    // the fused backward's control block holds one counter per (b, h, query
-    // block) of a chunk
-    const long n_qb = (s.T + 31) / 32;
-    if (chunk > 0 && (long)gpt_attn::bwd_fused_ctl_ints(s, chunk) * 4 > (long)gpt_attn::kCtlBytes)
-        chunk = (int)((gpt_attn::kCtlBytes / 4 - 32) / n_qb);
     void *ws = nullptr;
+    unsigned epoch = 0;
     hipError_t e = hipSuccess;
     if (noalloc)
     {
@@ -329,7 +386,7 @@ int backward(const char *op, bool noalloc, float *grad_x, float *D_cache, const 
                         "array (T <= 5760 fits)",
                         op, bytes, s.T, kScratchBytes);
         float *p = nullptr;
-        e = scratch_addr(&p);
+        e = scratch_addr(&p, &epoch);
         if (e != hipSuccess)
             return fail(GPT_HIP_ATTN_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", op,
                         hipGetErrorString(e));
@@ -337,7 +394,12 @@ int backward(const char *op, bool noalloc, float *grad_x, float *D_cache, const 
     }
     else
     {
-        e = workspace_get(&ws, gpt_attn::kCtlBytes + bytes, st);
+        e = workspace_get(&ws, &epoch, gpt_attn::kCtlBytes + bytes, st);
+        if (e == hipErrorStreamCaptureUnsupported)
+            return fail(GPT_HIP_ATTN_ENOMEM,
+                        "%s: the stream is capturing a graph and its dS workspace (%zu bytes) is not allocated "
+                        "yet: make one call on the stream before capturing, or use gpt_hip_attn_bwd_f32_noalloc",
+                        op, gpt_attn::kCtlBytes + bytes);
         if (e != hipSuccess)
             return fail(GPT_HIP_ATTN_ENOMEM, "%s: workspace of %zu bytes: %s", op, gpt_attn::kCtlBytes + bytes,
                         hipGetErrorString(e));
@@ -349,7 +411,11 @@ int backward(const char *op, bool noalloc, float *grad_x, float *D_cache, const 
     // path 3 asks for the two-launch split
     const int n_cu = gpt_attn::device_cu_count();
     if (path != 3 && gpt_attn::bwd_fused_d64_fits(s, chunk, n_cu))
-        e = gpt_attn::launch_bwd_fused_d64(grad_x, D_cache, lse, grad_y, y, qkv, dsw, ctl, n_cu, s, st);
+    {
+        const gpt_attn::FusedSync sync{epoch, g_wait_us.load(std::memory_order_relaxed) * wall_ticks_per_us(),
+                                       g_need_extra.load(std::memory_order_relaxed)};
+        e = gpt_attn::launch_bwd_fused_d64(grad_x, D_cache, lse, grad_y, y, qkv, dsw, ctl, n_cu, sync, s, st);
+    }
     else
         e = gpt_attn::launch_bwd_d64(grad_x, D_cache, lse, grad_y, y, qkv, dsw, chunk, s, st);
     if (e != hipSuccess)
@@ -499,6 +565,15 @@ int gpt_hip_attn_release_workspaces(void)
     const hipError_t e = workspace_release_device();
     if (e != hipSuccess)
         return fail(GPT_HIP_ATTN_ELAUNCH, "%s: %s", op, hipGetErrorString(e));
+    return 0;
+}
+
+int gpt_hip_attn_set_wait_limit(long long microseconds, int extra_need)
+{
+    if (extra_need < 0)
+        return fail(GPT_HIP_ATTN_EINVAL, "gpt_hip_attn_set_wait_limit: extra_need %d < 0", extra_need);
+    g_wait_us.store(microseconds < 0 ? kDefaultWaitUs : microseconds, std::memory_order_relaxed);
+    g_need_extra.store(extra_need, std::memory_order_relaxed);
     return 0;
 }
 

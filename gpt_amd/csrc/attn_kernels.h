@@ -73,25 +73,41 @@ size_t bwd_d64_workspace_bytes(const Shape &s, size_t cap, int *bh_per_chunk);
 hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
                           const float *qkv, float *ws, int bh_per_chunk, const Shape &s, hipStream_t st);
 
-// Control block of the persistent fused backward: 32 queue ints plus one
-// completion counter per (b, h, query block) of a chunk. It sits at the start
-// of the workspace, is zeroed when the workspace is allocated and is left
-// all zeros by every launch.
+// Control block of the one-launch fused backward (layout in
+// attn_bwd_fused.hip): a word of expired waits, then per (b, h, key group)
+// a contribution counter, a start mark and a mailbox. It sits at the start of
+// the workspace and is zeroed when the workspace is allocated; every launch
+// leaves its counters at 0, and marks and mailboxes of earlier launches are
+// told apart by the launch epoch.
 constexpr size_t kCtlBytes = size_t(1) << 20;
-// Control-block word that counts the fused backward's dQ waits that hit
-// their spin limit.
+// Control-block word that counts the fused backward's dQ waits that reached
+// their time limit.
 constexpr int kCtlWaitErrors = 16;
-size_t bwd_fused_ctl_ints(const Shape &s, int bh_per_chunk);
+// Per-(b, h, key group) words, each kind in a region of its own at a fixed
+// place, so that no launch reads another shape's marks as counters: cnt from
+// word kCtlCounters, mark from kCtlCounters + kCtlItems, mbox (uint64) from
+// kCtlCounters + 2 kCtlItems; at most kCtlItems (b, h, key group) per launch.
+constexpr int kCtlCounters = 32;
+constexpr int kCtlItems = (int)((kCtlBytes / 4 - kCtlCounters) / 4) & ~1;
 
-// Backward, head_dim 64, fp32 MFMA, deterministic, one launch (plus the D-row
-// kernel for T > 256): one dK/dV item per workgroup, then dQ items that start
-// on each query block as soon as its dS tiles are complete. Only for calls
-// whose whole grid is resident at once and needs one chunk
-// (bwd_fused_d64_fits). `ws` holds the dS tiles of all B * H (b, h), `ctl`
-// the control block (all zeros on entry and on exit); n_cu = compute units.
+// Per-launch parameters of the fused backward's dQ hand-over.
+struct FusedSync
+{
+    unsigned epoch;        // never 0; differs between consecutive launches on one control block
+    long long wait_ticks;  // wall-clock ticks (wall_clock64) a dQ wait may last
+    int need_extra;        // test hook: added to every awaited count (0 in normal use)
+};
+
+// Backward, head_dim 64, fp32 MFMA, deterministic, one launch for T <= 256:
+// one dK/dV item per workgroup, then dQ items that start on each pair of
+// query blocks as soon as its dS tiles are complete. Correct whatever part of
+// the grid is resident; taken for grids one round of the CUs holds, needing
+// one chunk (bwd_fused_d64_fits). `ws` holds the dS tiles of all B * H (b, h),
+// `ctl` the control block; n_cu = compute units.
 bool bwd_fused_d64_fits(const Shape &s, int bh_per_chunk, int n_cu);
 hipError_t launch_bwd_fused_d64(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
-                                const float *qkv, float *ws, int *ctl, int n_cu, const Shape &s, hipStream_t st);
+                                const float *qkv, float *ws, int *ctl, int n_cu, const FusedSync &sync,
+                                const Shape &s, hipStream_t st);
 
 // D = rowsum(dO * O) for head_dim 64 (bwd_rowdot_d64_kernel).
 hipError_t launch_bwd_rowdot_d64(float *D, const float *dy, const float *y, const Shape &s, hipStream_t st);

@@ -19,13 +19,15 @@
  *   - Softmax scale is 1/sqrt(d); the causal mask keeps key j <= query i.
  *   - `stream` is a hipStream_t passed as void*; NULL means the default stream.
  *     Work is enqueued asynchronously. The forward allocates nothing. The
- *     head_dim-64 backward uses a workspace (a 1 MiB control block, all
- *     zeros between calls, then the dS tiles: 4 KiB per 32x32 causal tile,
- *     28 MiB at B=16 T=256 H=12, at most 2 GiB per call: larger problems run
- *     in (b, h) chunks) that the library allocates on first use, one buffer
- *     per (device, stream), grows when a call needs more (after waiting for
- *     that stream) and keeps until the process ends; steady-state calls do
- *     not allocate.
+ *     head_dim-64 backward uses a workspace (a 1 MiB control block, then the
+ *     dS tiles: 4 KiB per 32x32 causal tile, 28 MiB at B=16 T=256 H=12, at
+ *     most 2 GiB per call: larger problems run in (b, h) chunks) that the
+ *     library allocates on first use, one buffer per (device, stream), grows
+ *     when a call needs more (after waiting for that stream) and keeps until
+ *     the process ends; steady-state calls do not allocate. A call that
+ *     would allocate while its stream is capturing a graph returns
+ *     GPT_HIP_ATTN_ENOMEM instead (make one call before capturing, or use
+ *     gpt_hip_attn_bwd_f32_noalloc).
  *   - Return 0 on success or a negative GPT_HIP_ATTN_E* code; the message of
  *     the last failure on the calling thread is kept for
  *     gpt_hip_attn_last_error(). Inputs are never modified.
@@ -97,16 +99,30 @@ int gpt_hip_attn_bwd_f32_noalloc(float *grad_x, float *D_cache, const float *lse
                                  int batch_size, int seq_len, int hidden_size, int num_heads,
                                  void *stream);
 
-/* Number of dQ waits in the one-launch backward (T <= 256) that gave up at
- * their spin limit, on the calling thread's current device, since the last
+/* Number of dQ waits in the one-launch backward (T <= 256) that reached
+ * their time limit, on the calling thread's current device, since the last
  * call; the counts are cleared. Waits for all work queued on the device
- * first (hipDeviceSynchronize). A wait ends once the dK/dV work it waits for
- * has stored its dS tiles, which every workgroup of the launch does without
- * waiting itself, so any correct run returns 0; a nonzero count means that
- * many dQ items read incomplete tiles (wrong dQ rows). Returns the count
- * (>= 0), or GPT_HIP_ATTN_ENODEV / GPT_HIP_ATTN_ELAUNCH. No reference
- * counterpart (the reference's dQ uses atomics and never waits). */
+ * first (hipDeviceSynchronize). A dQ item waits only for dK/dV work that has
+ * already started on the GPU, which stores its dS tiles without waiting for
+ * anything itself (work that has not started gets the dQ item handed over
+ * instead), so any correct run returns 0 whatever else shares the GPU; a
+ * nonzero count means that many dQ items read incomplete tiles (wrong dQ
+ * rows). A launch with such a wait still leaves the control block ready for
+ * the next call. Returns the count (>= 0), or GPT_HIP_ATTN_ENODEV /
+ * GPT_HIP_ATTN_ELAUNCH. No reference counterpart (the reference's dQ uses
+ * atomics and never waits). */
 int gpt_hip_attn_wait_timeouts(void);
+
+/* Test hook for the one-launch backward's dQ waits (process-wide, read at
+ * each launch; not thread-safe). `microseconds` is the time limit of one
+ * wait (default 1000000; a negative value restores it); `extra_need` is
+ * added to every count a dQ item waits for (default 0), so that with
+ * extra_need > 0 every wait that is not skipped runs to the limit: this is
+ * how tests drive the timeout path without stalling the GPU. Results of a
+ * launch made with extra_need > 0 are undefined (its waits time out); the
+ * next launch with the defaults is correct. Returns 0, or
+ * GPT_HIP_ATTN_EINVAL for extra_need < 0. No reference counterpart. */
+int gpt_hip_attn_set_wait_limit(long long microseconds, int extra_need);
 
 /* Frees the default backward's dS workspaces on the calling thread's current
  * device. gpt_hip_attn_bwd_f32 keeps one grow-only workspace per (device,

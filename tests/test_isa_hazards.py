@@ -99,3 +99,88 @@ def test_scanner_finds_the_pattern():
     assert len(hazards(bad)) == 1
     assert hazards(ok) == []
     assert len(hazards(glob)) == 1
+
+
+def kernel_bodies(asm, name_part):
+    """Instruction lists of the functions whose symbol contains name_part."""
+    out, cur = {}, None
+    for line in asm.splitlines():
+        m = re.match(r"^[0-9a-f]+ <(\S+)>:", line)
+        if m:
+            cur = m.group(1) if name_part in m.group(1) else None
+            if cur:
+                out[cur] = []
+            continue
+        if cur is None:
+            continue
+        ins = line.split("//")[0].strip()
+        # objdump lines: "<instruction> ... // <address>: <encoding>"
+        if ins and re.match(r"^[a-z_]", ins):
+            out[cur].append(ins)
+    return out
+
+
+WAIT_VM = re.compile(r"^s_waitcnt\b.*\bvmcnt\((\d+)\)")
+
+
+def bump_order_violations(instrs):
+    """Counter bumps of the fused backward's walk (the global_atomic_add
+    before the mailbox exchange) that do not follow, in program order, a
+    workgroup barrier with no vector store between the two, preceded since the
+    barrier before it by a vmcnt wait of at most 8 (what the kernel's dS
+    hand-over relies on: each wave waits for its earlier dS stores, the
+    barrier gathers the waves, then one thread bumps)."""
+    close = next((k for k, s in enumerate(instrs) if s.startswith("global_atomic_swap_x2")), None)
+    assert close is not None, "no mailbox exchange found"
+    bumps = [k for k, s in enumerate(instrs[:close]) if s.startswith("global_atomic_add ")]
+    bad = []
+    for k in bumps:
+        b = max((j for j in range(k) if instrs[j].startswith("s_barrier")), default=None)
+        if b is None:
+            bad.append(f"bump at {k}: no barrier before it")
+            continue
+        stores = [s for s in instrs[b + 1:k] if re.match(r"(global|buffer|flat)_store", s)]
+        if stores:
+            bad.append(f"bump at {k}: store between barrier and bump: {stores[0]}")
+        b0 = max((j for j in range(b) if instrs[j].startswith("s_barrier")), default=-1)
+        waits = [int(m.group(1)) for s in instrs[b0 + 1:b] for m in [WAIT_VM.match(s)] if m]
+        if not waits or min(waits) > 8:
+            bad.append(f"bump at {k}: no vmcnt(<= 8) wait before its barrier")
+    return bumps, bad
+
+
+def test_fused_backward_bumps_follow_the_store_wait_and_barrier():
+    lib = LIBS[0]
+    if not os.path.exists(lib):
+        pytest.skip("library not built")
+    import tempfile
+
+    found = 0
+    with tempfile.TemporaryDirectory() as d:
+        for k, obj in enumerate(gfx950_code_objects(lib)):
+            f = os.path.join(d, f"co{k}.o")
+            open(f, "wb").write(obj)
+            asm = subprocess.run([OBJDUMP, "-d", "--mcpu=gfx950", f], capture_output=True, text=True,
+                                 check=True).stdout
+            for name, instrs in kernel_bodies(asm, "bwd_fused_d64_kernel").items():
+                bumps, bad = bump_order_violations(instrs)
+                assert len(bumps) >= 2, (name, len(bumps))
+                assert not bad, (name, bad)
+                found += 1
+    assert found == 2  # both instantiations
+
+
+def test_bump_checker_flags_a_moved_atomic():
+    ok = ["global_store_dword v[1:2], v3, off sc1", "s_waitcnt vmcnt(8)", "s_barrier",
+          "global_atomic_add v[4:5], v6, off offset:128", "global_atomic_swap_x2 v[1:2], v0, v[2:3], s[0:1]"]
+    moved = ["global_store_dword v[1:2], v3, off sc1", "s_waitcnt vmcnt(8)",
+             "global_atomic_add v[4:5], v6, off offset:128", "s_barrier",
+             "global_atomic_swap_x2 v[1:2], v0, v[2:3], s[0:1]"]
+    sunk = ["s_waitcnt vmcnt(8)", "s_barrier", "global_store_dword v[1:2], v3, off sc1",
+            "global_atomic_add v[4:5], v6, off offset:128", "global_atomic_swap_x2 v[1:2], v0, v[2:3], s[0:1]"]
+    nowait = ["s_barrier", "global_store_dword v[1:2], v3, off sc1", "s_waitcnt vmcnt(12)", "s_barrier",
+              "global_atomic_add v[4:5], v6, off offset:128", "global_atomic_swap_x2 v[1:2], v0, v[2:3], s[0:1]"]
+    assert bump_order_violations(ok)[1] == []
+    assert bump_order_violations(moved)[1]
+    assert bump_order_violations(sunk)[1]
+    assert bump_order_violations(nowait)[1]
