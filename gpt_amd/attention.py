@@ -200,10 +200,12 @@ def wait_timeouts() -> int:
 
 
 def set_wait_limit(microseconds: int = -1, extra_need: int = 0) -> None:
-    """Test hook for the one-launch backward's dQ waits: time limit of one
-    wait (negative = the default, one second) and a count added to every
-    awaited count (extra_need > 0 makes every such wait run to the limit).
-    Process-wide; read at each launch."""
+    """Test hook for the one-launch backward's dQ waits: the owners' wait
+    before they hand an item to the orphan runners (default 50 us) and the
+    runners' safety limit for an item's counts (default one second), both set
+    to `microseconds` (negative restores the defaults), and a count added to
+    every awaited count (extra_need > 0 makes every owner hand its item over
+    and every runner's wait expire). Process-wide; read at each launch."""
     _check(load_library().gpt_hip_attn_set_wait_limit(int(microseconds), int(extra_need)))
 
 

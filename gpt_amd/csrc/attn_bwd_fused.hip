@@ -19,9 +19,8 @@
 //     finish the high blocks (the ones with the most dQ work) first. After
 //     the barrier that ends the step of block i, each wave's dS stores of the
 //     block before (i + 1) are complete (the step's vm_wait covered them),
-//     and one thread adds 1 to the counter of the dQ item that covers block
-//     i + 1 (item (i + 1) / 2); the last block's is bumped after a final
-//     wait.
+//     and one thread adds 1 to the completion counter of (b, h, i + 1); the
+//     last block's counter is bumped after a final wait.
 //   dQ work of query blocks, done by the workgroups of the same
 //     (b, h) once their dK/dV item is done: key group J forms dQ of its own
 //     diagonal blocks 2J + 1 and 2J. Those are the last blocks it walks, and
@@ -43,38 +42,33 @@
 // stores it covers have completed, so a dQ item that sees a complete count
 // reads complete tiles.
 //
-// Forward progress does not depend on which workgroups are resident. A dQ
-// item K of (b, h) needs the dS tiles of key groups 0..K, and a workgroup
-// waits for them only while every one of those key groups has started: a
-// started dK/dV item runs to its end without waiting for anything, so such a
-// wait ends. When a contributor has not started (another kernel or process
-// holds CUs, the grid is larger than one resident round, the dispatcher
-// places workgroups in another order), the owner does not wait: it posts the
-// item to that key group's mailbox and moves on, and the key group runs the
-// item after its own (its walk has then stored every tile it contributes;
-// it decides again for the others). Per (b, h, key group) the control block
-// holds
-//   cnt[K]   contributions to dQ item K: one per (key group, block) whose dS
-//            tile stores have completed (2 (K + 1) in all, K + 1 for a last
-//            item with one block);
-//   mark[J]  the launch epoch, stored when key group J's workgroup starts;
-//   mbox[J]  epoch << 32 | kMboxClosed | bit K per item posted to J; J
-//            closes it with an exchange when its walk is done, which also
-//            returns the items posted to it. A post is a compare-and-swap
-//            that fails on a closed mailbox, so every posted item is seen by
-//            exactly one close.
-// The launch epoch (host-supplied, never 0, different for consecutive
-// launches on one control block) makes the marks and mailboxes of earlier
-// launches stale without clearing them. The one who runs item K subtracts
-// its need from cnt[K] afterwards, so every launch leaves the counters at 0
-// once its own bumps have landed. A wait also carries a time limit, a safety
-// net that no schedule reaches; when it expires the item counts an error in
-// the control block and computes from whatever is there.
+// Forward progress does not depend on which workgroups are resident. The
+// owner of a dQ item waits for its counts only for a bounded time (tens of
+// microseconds; in a launch whose grid is resident at once the counts are
+// complete long before). If a contributing key group has not run yet
+// (another kernel or process holds CUs, or the dispatcher placed work in
+// another order), the owner marks its item an orphan and ends, which frees
+// its slot. A few extra workgroups at the end of the grid (kOrphanRunners)
+// wait until every main workgroup of their (b, h) pairs has made its
+// decision (done counters), then run the orphans. No main workgroup ever waits for them, so every wait
+// ends; an orphan's counts are complete by then (its contributors walked
+// before deciding), and its dQ sums run in the same order, so the result is
+// the same bits whoever runs an item. Each counter is released by
+// subtracting its need once the item has run, so every launch leaves the
+// counters at 0 once its own bumps have landed. The runners' waits carry a
+// long time limit as a safety net that no schedule reaches; when it expires
+// it counts an error in the control block and the item computes from
+// whatever is there.
 //
-// Control block (int32 words, zeroed once when the workspace is allocated;
-// each region at a fixed place whatever the shape, M = kCtlItems):
-//   [16]  expired waits   [32, 32 + M) cnt   [32 + M, 32 + 2M) mark
-//   [32 + 2M, 32 + 4M) mbox (uint64); index (b, h) * key groups + J
+// Control block (int32 words, zeroed when the workspace is allocated; each
+// region at a fixed place whatever the shape, M = kCtlItems):
+//   [16] expired safety waits
+//   [32, 32 + M) completion counters, (b, h) * n_qb + block
+//   [32 + M, 32 + 2M) orphan flags, (b, h) * key groups + J: the epoch of
+//   the launch that made item J of (b, h) an orphan
+//   [32 + 2M, 32 + 3M) done counters, (b, h): its main workgroups that have
+//   decided (one counter per (b, h), so that these atomics do not all meet
+//   on one word); released by the runners
 #include "attn_common.h"
 #include "attn_kernels.h"
 
@@ -89,10 +83,6 @@ namespace {
 // pass measure as fast or faster).
 constexpr int kMaxFusedKeyGroups = 4;
 
-// Mailbox word: bit 16 = closed (the key group's walk is done), bits 0..3 =
-// dQ items posted to it (items are key groups 1..3 of the same (b, h)).
-constexpr unsigned long long kMboxClosed = 1ull << 16;
-constexpr unsigned long long kMboxItems = 0xFull;
 
 // dS tile stores / loads coherent at device scope (sc1).
 constexpr int kSc1 = 16;
@@ -111,53 +101,10 @@ __device__ __forceinline__ int load_agent(const int *p)
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Decides, for the calling thread's workgroup, whether it runs dQ item K of
-// one (b, h) now (true) or has posted it to the mailbox of a key group that
-// has not started or not finished its walk (false). `self` is the key group
-// whose walk this workgroup has finished (a contributor that needs no
-// check). Called by one thread.
-__device__ bool dq_claim(int *cnt_bh, const unsigned *mark_bh, unsigned long long *mbox_bh, int *errors, int K,
-                         int self, int need, unsigned epoch, long long wait_ticks)
-{
-    if (load_agent(cnt_bh + K) >= need)
-        return true;
-    for (int jp = 0; jp < K; ++jp)
-    {
-        if (jp == self || __hip_atomic_load(mark_bh + jp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch)
-            continue;  // started: its walk ends without waiting for anything
-        unsigned long long x = __hip_atomic_load(mbox_bh + jp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (;;)
-        {
-            const bool cur = (unsigned)(x >> 32) == epoch;
-            if (cur && (x & kMboxClosed))
-                break;  // its walk is done; its bumps are landing
-            const unsigned long long nx = (cur ? x : (unsigned long long)epoch << 32) | (1ull << K);
-            if (__hip_atomic_compare_exchange_strong(mbox_bh + jp, &x, nx, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT))
-                return false;
-        }
-    }
-    // every contributor has started: wait for their bumps
-    const long long t0 = (long long)wall_clock64();
-    while (load_agent(cnt_bh + K) < need)
-    {
-        if ((long long)wall_clock64() - t0 > wait_ticks)
-        {
-            __hip_atomic_fetch_add(errors, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-    }
-    return true;
-}
-
 }  // namespace
 
-// HELP (grids of at most 2 workgroups per CU) needs only 2 waves per SIMD,
-// which leaves it the registers that its longer last step takes without
-// spilling.
 template <bool FUSE_D, bool HELP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HELP ? 2 : 3))) void bwd_fused_d64_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void bwd_fused_d64_kernel(
     float *__restrict__ grad_x, float *__restrict__ dsw, int *__restrict__ ctl, const float *__restrict__ lse,
     float *__restrict__ Dv, const float *__restrict__ dy, const float *__restrict__ y, const float *__restrict__ qkv,
     int T, int C, int H, int bh0, int BHc, int n_qb, float c2, float scale, int n_cu, FusedSync sync)
@@ -168,15 +115,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HELP ? 2 : 
     const int n_kg = (n_qb + 1) / 2;
     const uint32_t Wb = 12u * (uint32_t)C, Cb = 4u * (uint32_t)C, Hb = 4u * (uint32_t)H;
     const long tiles = (long)n_qb * (n_qb + 1) / 2;
-    // control block (layout above)
     int *cnt = ctl + kCtlCounters;
-    // one contribution to a dQ item's count, by one thread after the barrier
-    // that follows every wave's wait for the dS stores it covers (the signal
-    // fence keeps the compiler from moving the atomic above those)
-    auto bump = [&](int *c) {
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
+    unsigned *orphan = reinterpret_cast<unsigned *>(ctl + kCtlCounters + kCtlItems);
+    int *done = ctl + kCtlCounters + 2 * kCtlItems;
 
     // LDS: the dK/dV item's staging buffers (one array per buffer, so that
     // the compiler sees that loads landing in one buffer do not alias reads of
@@ -202,7 +143,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HELP ? 2 : 
                                   : make_rsrc(Dv + (long)b * T * H + h, (uint32_t)(((long)T * H - h) * 4));
         float *ws = dsw + (long)bhl * tiles * 1024;
         float *gx_out = grad_x + (long)b * T * 3L * C + (long)h * 64;
-        int *cnt_bh = cnt + (long)bhl * n_kg;  // bumped per block i: item i / 2
+        int *cnt_bh = cnt + (long)bhl * n_qb;
 
         auto bufs = [&](auto buf_c) {
             constexpr int buf = decltype(buf_c)::value;
@@ -311,6 +252,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HELP ? 2 : 
                 d_rows(i_top, BufIdx<1>{});
         }
         __syncthreads();
+        int done_prev = -1;  // block whose dS stores the next barrier covers
         // One query block. GEN: a diagonal block (i = 2J, 2J + 1), which tests
         // for skipped tiles and zero halves and applies the causal mask.
         // Keys whose units a wave computes in a diagonal step, and halves it
@@ -486,9 +428,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HELP ? 2 : 
             }
             lds_barrier();
             // every wave's dS stores of the previous block are complete
-            // this barrier covers the dS stores of the block before (i + 1)
-            if (tid == 0 && i < i_top)
-                bump(cnt_bh + ((i + 1) >> 1));
+            if (tid == 0 && done_prev >= 0)
+                __hip_atomic_fetch_add(cnt_bh + done_prev, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            done_prev = i;
         };
         for (int i = i_top; i >= i_lo + 2; --i)
         {
@@ -554,7 +496,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HELP ? 2 : 
             lds_dma_wait();
             lds_barrier();
             if (tid == 0)
-                bump(cnt_bh + J);  // the last block, i_lo = 2J
+                __hip_atomic_fetch_add(cnt_bh + done_prev, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             // wave 2's partial through buffer 1's Q tile (free: the last step
             // read buffer 0, and every wave's staging loads have landed)
             float4 *part = reinterpret_cast<float4 *>(sq1) + lane;
@@ -588,7 +530,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HELP ? 2 : 
             lds_dma_wait();
             lds_barrier();
             if (tid == 0)
-                bump(cnt_bh + J);  // the last block, i_lo = 2J
+                __hip_atomic_fetch_add(cnt_bh + done_prev, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
             // register r of lane l: key kw0 + 4 g4 + r, dims 4 c16 + e
 #pragma unroll
@@ -606,12 +548,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HELP ? 2 : 
     };
 
     // --------------------------------------------------------------- dQ item
-    // dQ of key group K's two diagonal blocks (2K + 1, 2K) as one item, once
-    // their dS tiles are complete (dq_claim): dQ_i = scale * sum_{j<=i} dS_ij
-    // K_j on v_mfma_f32_32x32x2_f32, the units of block 2K + 1 then those of
-    // block 2K split over the 4 waves in contiguous ranges (a wave's range may
-    // cover both blocks: two sets of accumulators), one half-unit of operands
-    // ahead; each block's 4 partials added through LDS in wave order.
+    // dQ of key group J's two diagonal blocks (2J + 1, 2J) as one item, once
+    // both blocks' counters have reached the number of key groups that cover
+    // them (J + 1; see the schedule): dQ_i = scale * sum_{j<=i} dS_ij K_j on
+    // v_mfma_f32_32x32x2_f32, the units of block 2J + 1 then those of block
+    // 2J split over the 4 waves in contiguous ranges (a wave's range may cover
+    // both blocks: two sets of accumulators), one half-unit of operands ahead;
+    // each block's 4 partials added through LDS in wave order.
     auto dq_both = [&](const int J, const int bhl) {
         const int bh = bh0 + bhl;
         const int b = bh / H, h = bh % H;
@@ -724,15 +667,100 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HELP ? 2 : 
         reduce(qlo, c0, c1);
     };
 
+    // ---------------------------------------------------------- dQ claims
+    // Whether a dQ item's counts are complete, by thread 0 of the workgroup:
+    // both blocks' counters (block 2J + 1 only if it exists) at `need` or
+    // more, waiting at most `ticks` of wall-clock time (then false).
+    auto counts_complete = [&](const int *cnt_b, const int J, const int need, const long long ticks) {
+        const int qhi = 2 * J + 1, qlo = 2 * J;
+        const long long t0 = (long long)wall_clock64();
+        for (;;)
+        {
+            const int c_lo = load_agent(cnt_b + qlo);
+            const int c_hi = qhi < n_qb ? load_agent(cnt_b + qhi) : need;
+            if (c_lo >= need && c_hi >= need)
+                return true;
+            if ((long long)wall_clock64() - t0 > ticks)
+                return false;
+            __builtin_amdgcn_s_sleep(2);
+        }
+    };
+    // back to 0 once every bump of this launch has landed
+    auto release = [&](int *cnt_b, const int J) {
+        if (tid == 0)
+        {
+            const int qhi = 2 * J + 1, qlo = 2 * J;
+            __hip_atomic_fetch_add(cnt_b + qlo, -(J + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (qhi < n_qb)
+                __hip_atomic_fetch_add(cnt_b + qhi, -(J + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    };
+    __shared__ int s_run;
+
     // ------------------------------------------------------------ schedule
-    // the dK/dV item of this workgroup: J-major, heaviest first, (b, h)
-    // fastest; when the whole grid is resident at 3 per CU, CU c hosts
-    // workgroups c, c + n_cu, c + 2 n_cu, and the middle round takes its items
-    // in reverse (in blocks of 8, which keeps each (b, h) on one XCD), so that
-    // every CU gets one heavy, one light and one middle item
+    if ((int)blockIdx.x >= sync.n_main)
+    {
+        // Orphan runner r of the grid's last kOrphanRunners workgroups, for
+        // (b, h) pairs bh_lo .. bh_hi - 1: once every main workgroup of them
+        // has decided (their done counters reach the key-group count), run
+        // their orphans, then release the done counters.
+        __shared__ int s_list[256], s_n;
+        const int runners = (int)gridDim.x - sync.n_main, r = (int)blockIdx.x - sync.n_main;
+        const int per = (BHc + runners - 1) / runners;
+        const int bh_lo = r * per, bh_hi = bh_lo + per < BHc ? bh_lo + per : BHc;
+        for (int bh = bh_lo + tid; bh < bh_hi; bh += 256)
+        {
+            const long long t0 = (long long)wall_clock64();
+            while (load_agent(done + bh) < n_kg)
+            {
+                if ((long long)wall_clock64() - t0 > sync.done_ticks)
+                {
+                    __hip_atomic_fetch_add(ctl + kCtlWaitErrors, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(8);
+            }
+        }
+        if (tid == 0)
+            s_n = 0;
+        __syncthreads();
+        for (int base = bh_lo * n_kg; base < bh_hi * n_kg; base += 256)
+        {
+            const int idx = base + tid;
+            if (idx < bh_hi * n_kg &&
+                __hip_atomic_load(orphan + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == sync.epoch)
+                s_list[atomicAdd(&s_n, 1)] = idx;
+            __syncthreads();
+            const int n = s_n;
+            for (int k = 0; k < n; ++k)
+            {
+                const int item = s_list[k], J = item % n_kg, bhl = item / n_kg;
+                int *cnt_b = cnt + (long)bhl * n_qb;
+                if (tid == 0 && !counts_complete(cnt_b, J, J + 1 + sync.need_extra, sync.safety_ticks))
+                    __hip_atomic_fetch_add(ctl + kCtlWaitErrors, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __syncthreads();
+                dq_both(J, bhl);
+                release(cnt_b, J);
+            }
+            __syncthreads();
+            if (tid == 0)
+                s_n = 0;
+            __syncthreads();
+        }
+        // back to 0 once every main workgroup's count has landed
+        for (int bh = bh_lo + tid; bh < bh_hi; bh += 256)
+            __hip_atomic_fetch_add(done + bh, -n_kg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    // Main workgroup: the dK/dV item of this workgroup: J-major, heaviest
+    // first, (b, h) fastest; when the whole grid is resident at 3 per CU,
+    // CU c hosts workgroups c, c + n_cu, c + 2 n_cu, and the middle round
+    // takes its items in reverse (in blocks of 8, which keeps each (b, h) on
+    // one XCD), so that every CU gets one heavy, one light and one middle
+    // item
     {
         int item = (int)blockIdx.x;
-        const int G = (int)gridDim.x;
+        const int G = sync.n_main;
         if (n_cu > 0 && n_cu % 8 == 0 && G % n_cu == 0 && G / n_cu <= 3)
         {
             const int r = item / n_cu;
@@ -741,14 +769,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HELP ? 2 : 
                 c = (n_cu / 8 - 1 - c / 8) * 8 + (c & 7);
             item = r * n_cu + c;
         }
-        const int J0 = item / BHc, bhl0 = item % BHc;
+        const int J = item / BHc, bhl = item % BHc;
         // Wave priority by weight: the heaviest key groups (the longest chains
         // of steps) issue first, so that their chains run at about a lone
         // wave's speed while the lighter items fill the gaps (12-layer step,
         // A/B on one box: heavy first 1.052 ms, no priorities 1.055 ms, light
         // first 1.121 ms).
         {
-            const int pr = n_kg - 1 - J0;
+            const int pr = n_kg - 1 - J;
             if (pr >= 3)
                 __builtin_amdgcn_s_setprio(3);
             else if (pr == 2)
@@ -756,84 +784,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HELP ? 2 : 
             else if (pr == 1)
                 __builtin_amdgcn_s_setprio(1);
         }
-        // control block of this (b, h): the cnt, mark and mbox words of its
-        // key groups
-        auto mark_of = [&](int bh) { return reinterpret_cast<unsigned *>(cnt + kCtlItems) + (long)bh * n_kg; };
-        auto mbox_of = [&](int bh) {
-            return reinterpret_cast<unsigned long long *>(cnt + 2 * kCtlItems) + (long)bh * n_kg;
-        };
-        // started: an owner waiting for this key group's bumps may wait (a
-        // wave-uniform branch, all lanes storing the same word: a tid == 0
-        // branch here made the compiler spill VGPRs in the walk)
-        if (w == 0)
-            __hip_atomic_store(mark_of(bhl0) + J0, sync.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // What the dQ phase needs waits in LDS through the walk: the launch
-        // parameters, and the item itself, read back from there so that the
-        // compiler cannot share address arithmetic of the dQ phase with the
-        // walk (kept in registers through the walk, either made it spill
-        // VGPRs in the diagonal steps).
-        __shared__ long long s_par[5];
-        if (w == 0)
-        {
-            s_par[0] = sync.epoch;
-            s_par[1] = sync.wait_ticks;
-            s_par[2] = sync.need_extra;
-            s_par[3] = J0;
-            s_par[4] = bhl0;
-        }
-        dkdv_item(J0, bhl0);
-        const unsigned epoch = (unsigned)s_par[0];
-        const long long wait_ticks = s_par[1];
-        const int need_extra = (int)s_par[2];
-        const int J = (int)s_par[3], bhl = (int)s_par[4];
-        int *const cnt_bh = cnt + (long)bhl * n_kg;
-        unsigned *const mark_bh = mark_of(bhl);
-        unsigned long long *const mbox_bh = mbox_of(bhl);
-        // walk done: close the mailbox; the items posted to it come back
-        __shared__ int s_run, s_next, s_todo;
+        dkdv_item(J, bhl);
+        // dQ of this key group's own diagonal blocks (2J + 1, then 2J), at
+        // the lowest priority (see above). Key group 0's blocks 0 and 1 take
+        // dS from key group 0 alone, whose stores completed before the
+        // barrier that ended its walk: no wait. Otherwise thread 0 waits a
+        // bounded time for the counts; if they are still short, the item
+        // becomes an orphan (flag stored, its completion awaited, before the
+        // done counter moves, so a runner that sees the count sees the flag).
+        __builtin_amdgcn_s_setprio(0);
+        int *cnt_b = cnt + (long)bhl * n_qb;
         if (tid == 0)
         {
-            const unsigned long long posted = __hip_atomic_exchange(
-                mbox_bh + J, ((unsigned long long)epoch << 32) | kMboxClosed, __ATOMIC_RELAXED,
-                __HIP_MEMORY_SCOPE_AGENT);
-            s_todo = (unsigned)(posted >> 32) == epoch ? (int)(posted & kMboxItems) : 0;
+            bool run = true;
+            if (J > 0 && !counts_complete(cnt_b, J, J + 1 + sync.need_extra, sync.wait_ticks))
+            {
+                run = false;
+                const unsigned old =
+                    __hip_atomic_exchange(orphan + (long)bhl * n_kg + J, sync.epoch, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+                asm volatile("" ::"v"(old));  // the flag is in place before the done counter moves
+            }
+            __hip_atomic_fetch_add(done + bhl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_run = run;
         }
-        // dQ items, at the lowest priority (see above): this key group's own
-        // diagonal blocks (2J + 1, then 2J), then any posted to it, in
-        // increasing order. Item 0 takes dS from key group 0 alone, whose
-        // stores completed before the barrier that ended its walk: no claim.
-        // The items still to do stay in LDS (s_todo, read by thread 0 only):
-        // a loop that kept them in registers made the compiler spill VGPRs
-        // in the walk.
-        __builtin_amdgcn_s_setprio(0);
-        int K = J;
-        for (;;)
+        __syncthreads();  // the decision is out; the dK/dV item's LDS is free
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (__builtin_amdgcn_readfirstlane(s_run))
         {
-            const int need = (K + 1) * (2 * K + 1 < n_qb ? 2 : 1);
-            if (tid == 0)
-                s_run = K == 0 || dq_claim(cnt_bh, mark_bh, mbox_bh, ctl + kCtlWaitErrors, K, J, need + need_extra,
-                                           epoch, wait_ticks);
-            __syncthreads();  // the decision is out (and the dK/dV item's LDS free)
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            if (__builtin_amdgcn_readfirstlane(s_run))  // the same in every wave
-            {
-                dq_both(K, bhl);
-                if (tid == 0)  // back to 0 once every bump of this launch has landed
-                    __hip_atomic_fetch_add(cnt_bh + K, -need, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            // next item (s_run is written again only after the barrier below,
-            // which every wave reaches after reading it)
-            if (tid == 0)
-            {
-                const unsigned todo = (unsigned)s_todo;
-                s_next = todo ? __builtin_ctz(todo) : -1;
-                s_todo = (int)(todo & (todo - 1));
-            }
-            __syncthreads();
-            K = __builtin_amdgcn_readfirstlane(s_next);
-            if (K < 0)
-                break;
-            __syncthreads();  // every wave has read s_next before it is written again
+            dq_both(J, bhl);
+            release(cnt_b, J);
         }
     }
 }
@@ -860,24 +840,26 @@ bool bwd_fused_d64_fits(const Shape &s, int bh_per_chunk, int n_cu)
 {
     // Correct at any grid size (no wait depends on residency); taken where it
     // measured fastest, grids that one round of the CUs holds, with one chunk
-    // and a control block that fits.
-    const long n_kg = (s.T + 63) / 64;
+    // and a control block that holds its counters and flags.
+    const long n_kg = (s.T + 63) / 64, n_qb = (s.T + 31) / 32;
     return n_cu > 0 && s.T <= 64 * kMaxFusedKeyGroups && bh_per_chunk >= s.B * s.H &&
-           (long)s.B * s.H * n_kg <= kCtlItems &&
-           (long)s.B * s.H * n_kg <= (long)fused_per_cu() * n_cu;
+           (long)s.B * s.H * n_qb <= kCtlItems && (long)s.B * s.H * n_kg <= (long)fused_per_cu() * n_cu;
 }
+
+int bwd_fused_d64_main_workgroups(const Shape &s) { return (s.T + 63) / 64 * s.B * s.H; }
 
 hipError_t launch_bwd_fused_d64(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
                                 const float *qkv, float *ws, int *ctl, int n_cu, const FusedSync &sync,
                                 const Shape &s, hipStream_t st)
 {
-    const int n_qb = (s.T + 31) / 32, n_kg = (s.T + 63) / 64;
+    const int n_qb = (s.T + 31) / 32;
     const int BH = s.B * s.H;
     const float scale = 1.0f / sqrtf(64.f);
-    const dim3 g((unsigned)(n_kg * BH));
+    const int n_main = bwd_fused_d64_main_workgroups(s);
+    const dim3 g((unsigned)(n_main + kOrphanRunners));
     // T <= 256 (bwd_fused_d64_fits): the D rows are computed in the kernel;
     // grids of at most 2 workgroups per CU share the last step's work out
-    if (n_kg * BH <= 2 * n_cu)
+    if (n_main <= 2 * n_cu)
         launch_timed(kKindFused, bwd_fused_d64_kernel<true, true>, g, dim3(256), st, grad_x, ws, ctl, lse, D, dy, y,
                      qkv, s.T, s.C, s.H, 0, BH, n_qb, scale * kLog2e, scale, n_cu, sync);
     else

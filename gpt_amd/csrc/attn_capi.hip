@@ -28,10 +28,14 @@ thread_local char g_err[512] = "";
 // only, 2 atomic-dQ backward, 3 two-launch backward at every T; read once per
 // call
 std::atomic<int> g_path{0};
-// Time limit of the fused backward's dQ waits, in microseconds, and the test
+// Time limits of the fused backward's dQ waits, in microseconds, and the test
 // hook's extra count (gpt_hip_attn_set_wait_limit).
-constexpr long long kDefaultWaitUs = 1000000;
-std::atomic<long long> g_wait_us{kDefaultWaitUs};
+// Default limits: how long the owner of a dQ item waits before it hands the
+// item to the orphan runners, and the runners' safety limit.
+constexpr long long kDefaultOwnerWaitUs = 50;
+constexpr long long kDefaultSafetyUs = 1000000;
+std::atomic<long long> g_owner_wait_us{kDefaultOwnerWaitUs};
+std::atomic<long long> g_safety_us{kDefaultSafetyUs};
 std::atomic<int> g_need_extra{0};
 
 // Wall-clock ticks (wall_clock64) per microsecond of the current device.
@@ -155,10 +159,11 @@ __global__ void zero_ints_kernel(int *p, int n)
 }
 
 // Device buffer of at least `bytes` bytes for the backward on `st`, and the
-// epoch for its next fused launch. Refuses (hipErrorStreamCaptureUnsupported)
-// to allocate while `st` is capturing a graph: such callers take
-// gpt_hip_attn_bwd_f32_noalloc, or make one call before capturing.
-hipError_t workspace_get(void **out, unsigned *epoch, size_t bytes, hipStream_t st)
+// epoch of its next fused launch (advanced when `fused`). Refuses
+// (hipErrorStreamCaptureUnsupported) to allocate while `st` is capturing a
+// graph: such callers take gpt_hip_attn_bwd_f32_noalloc, or make one call
+// before capturing.
+hipError_t workspace_get(void **out, unsigned *epoch, bool fused, size_t bytes, hipStream_t st)
 {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -195,6 +200,7 @@ hipError_t workspace_get(void **out, unsigned *epoch, size_t bytes, hipStream_t 
             w->p = nullptr;
             w->bytes = 0;
         }
+        w->epoch = 0;  // a new control block is zeroed below
         e = hipMalloc(&w->p, bytes);
         if (e == hipSuccess)  // the fused backward's control block starts out zeroed
         {
@@ -212,7 +218,8 @@ hipError_t workspace_get(void **out, unsigned *epoch, size_t bytes, hipStream_t 
         w->bytes = bytes;
     }
     *out = w->p;
-    w->epoch = next_epoch(w->epoch);
+    if (fused)
+        w->epoch = next_epoch(w->epoch);
     *epoch = w->epoch;
     return hipSuccess;
 }
@@ -262,14 +269,16 @@ struct ScratchAddr
     std::once_flag once;
     hipError_t err = hipSuccess;
     float *p = nullptr;
-    std::atomic<unsigned> epoch{0};  // of the last fused-backward launch on its control block
+    std::mutex mu;
+    unsigned epoch = 0;  // of the last fused-backward launch on its control block
 };
 ScratchAddr g_scratch[kMaxDevices];
 
 // Device address of the current device's scratch array (looked up on the
 // first call per device, with that device current) and, when `epoch` is
-// given, the epoch for the next fused launch on its control block.
-hipError_t scratch_addr(float **out, unsigned *epoch = nullptr)
+// given, the epoch of its control block's next fused launch (advanced when
+// `fused`).
+hipError_t scratch_addr(float **out, unsigned *epoch = nullptr, bool fused = false)
 {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -288,11 +297,10 @@ hipError_t scratch_addr(float **out, unsigned *epoch = nullptr)
     *out = s.p;
     if (epoch)
     {
-        unsigned e = s.epoch.load(std::memory_order_relaxed), n;
-        do
-            n = next_epoch(e);
-        while (!s.epoch.compare_exchange_weak(e, n, std::memory_order_relaxed));
-        *epoch = n;
+        std::lock_guard<std::mutex> lock(s.mu);
+        if (fused)
+            s.epoch = next_epoch(s.epoch);
+        *epoch = s.epoch;
     }
     return hipSuccess;
 }
@@ -378,6 +386,10 @@ int backward(const char *op, bool noalloc, float *grad_x, float *D_cache, const 
     void *ws = nullptr;
     unsigned epoch = 0;
     hipError_t e = hipSuccess;
+    // the fused kernel for grids one round of the CUs holds (T <= 256), unless
+    // path 3 asks for the two-launch split
+    const int n_cu = gpt_attn::device_cu_count();
+    const bool fused = path != 3 && gpt_attn::bwd_fused_d64_fits(s, chunk, n_cu);
     if (noalloc)
     {
         if (chunk == 0)
@@ -386,7 +398,7 @@ int backward(const char *op, bool noalloc, float *grad_x, float *D_cache, const 
                         "array (T <= 5760 fits)",
                         op, bytes, s.T, kScratchBytes);
         float *p = nullptr;
-        e = scratch_addr(&p, &epoch);
+        e = scratch_addr(&p, &epoch, fused);
         if (e != hipSuccess)
             return fail(GPT_HIP_ATTN_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", op,
                         hipGetErrorString(e));
@@ -394,7 +406,7 @@ int backward(const char *op, bool noalloc, float *grad_x, float *D_cache, const 
     }
     else
     {
-        e = workspace_get(&ws, &epoch, gpt_attn::kCtlBytes + bytes, st);
+        e = workspace_get(&ws, &epoch, fused, gpt_attn::kCtlBytes + bytes, st);
         if (e == hipErrorStreamCaptureUnsupported)
             return fail(GPT_HIP_ATTN_ENOMEM,
                         "%s: the stream is capturing a graph and its dS workspace (%zu bytes) is not allocated "
@@ -407,13 +419,15 @@ int backward(const char *op, bool noalloc, float *grad_x, float *D_cache, const 
     // workspace layout: [control block | dS tiles]
     int *ctl = static_cast<int *>(ws);
     float *dsw = reinterpret_cast<float *>(static_cast<char *>(ws) + gpt_attn::kCtlBytes);
-    // the fused kernel where its grid is resident at once (T <= 256), unless
-    // path 3 asks for the two-launch split
-    const int n_cu = gpt_attn::device_cu_count();
-    if (path != 3 && gpt_attn::bwd_fused_d64_fits(s, chunk, n_cu))
+    if (fused)
     {
-        const gpt_attn::FusedSync sync{epoch, g_wait_us.load(std::memory_order_relaxed) * wall_ticks_per_us(),
-                                       g_need_extra.load(std::memory_order_relaxed)};
+        const long long tpu = wall_ticks_per_us();
+        const gpt_attn::FusedSync sync{epoch,
+                                       gpt_attn::bwd_fused_d64_main_workgroups(s),
+                                       g_need_extra.load(std::memory_order_relaxed),
+                                       g_owner_wait_us.load(std::memory_order_relaxed) * tpu,
+                                       g_safety_us.load(std::memory_order_relaxed) * tpu,
+                                       kDefaultSafetyUs * tpu};
         e = gpt_attn::launch_bwd_fused_d64(grad_x, D_cache, lse, grad_y, y, qkv, dsw, ctl, n_cu, sync, s, st);
     }
     else
@@ -534,10 +548,15 @@ int gpt_hip_attn_wait_timeouts(void)
     // (the lock is held throughout, so that no workspace is freed meanwhile)
     std::lock_guard<std::mutex> lock(g_ws_mu);
     int *blocks[kMaxWorkspaces + 1];
+    int ws_index[kMaxWorkspaces];
     int n = 0;
     for (int i = 0; i < g_ws_n && e == hipSuccess; ++i)
         if (g_ws[i].dev == dev && g_ws[i].p)
+        {
+            ws_index[n] = i;
             blocks[n++] = static_cast<int *>(g_ws[i].p);
+        }
+    const int n_ws = n;
     float *sp = nullptr;
     if (e == hipSuccess && scratch_addr(&sp) == hipSuccess && sp)
         blocks[n++] = reinterpret_cast<int *>(sp);
@@ -549,7 +568,18 @@ int gpt_hip_attn_wait_timeouts(void)
         int v = 0;
         e = hipMemcpy(&v, blocks[i] + gpt_attn::kCtlWaitErrors, sizeof(int), hipMemcpyDeviceToHost);
         if (e == hipSuccess && v != 0)
-            e = hipMemset(blocks[i] + gpt_attn::kCtlWaitErrors, 0, sizeof(int));
+        {
+            // a launch with an expired wait may have left counters or its
+            // done count off: start this control block afresh
+            e = hipMemset(blocks[i], 0, gpt_attn::kCtlBytes);
+            if (i < n_ws)
+                g_ws[ws_index[i]].epoch = 0;
+            else
+            {
+                std::lock_guard<std::mutex> sl(g_scratch[dev].mu);
+                g_scratch[dev].epoch = 0;
+            }
+        }
         total += v;
     }
     if (e != hipSuccess)
@@ -572,7 +602,8 @@ int gpt_hip_attn_set_wait_limit(long long microseconds, int extra_need)
 {
     if (extra_need < 0)
         return fail(GPT_HIP_ATTN_EINVAL, "gpt_hip_attn_set_wait_limit: extra_need %d < 0", extra_need);
-    g_wait_us.store(microseconds < 0 ? kDefaultWaitUs : microseconds, std::memory_order_relaxed);
+    g_owner_wait_us.store(microseconds < 0 ? kDefaultOwnerWaitUs : microseconds, std::memory_order_relaxed);
+    g_safety_us.store(microseconds < 0 ? kDefaultSafetyUs : microseconds, std::memory_order_relaxed);
     g_need_extra.store(extra_need, std::memory_order_relaxed);
     return 0;
 }

@@ -74,37 +74,43 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
                           const float *qkv, float *ws, int bh_per_chunk, const Shape &s, hipStream_t st);
 
 // Control block of the one-launch fused backward (layout in
-// attn_bwd_fused.hip): a word of expired waits, then per (b, h, key group)
-// a contribution counter, a start mark and a mailbox. It sits at the start of
-// the workspace and is zeroed when the workspace is allocated; every launch
-// leaves its counters at 0, and marks and mailboxes of earlier launches are
-// told apart by the launch epoch.
+// attn_bwd_fused.hip): a word of expired safety waits, then per (b, h, query
+// block) a completion counter, per (b, h, key group) an orphan flag and per
+// (b, h) a done counter. It sits at the start of the workspace and is zeroed
+// when the workspace is allocated; every launch leaves its counters at 0,
+// and flags of earlier launches are told apart by the launch epoch.
 constexpr size_t kCtlBytes = size_t(1) << 20;
-// Control-block word that counts the fused backward's dQ waits that reached
-// their time limit.
+// Control-block word that counts the fused backward's waits that reached
+// their safety time limit.
 constexpr int kCtlWaitErrors = 16;
-// Per-(b, h, key group) words, each kind in a region of its own at a fixed
-// place, so that no launch reads another shape's marks as counters: cnt from
-// word kCtlCounters, mark from kCtlCounters + kCtlItems, mbox (uint64) from
-// kCtlCounters + 2 kCtlItems; at most kCtlItems (b, h, key group) per launch.
+// Counters from word kCtlCounters, orphan flags from kCtlCounters +
+// kCtlItems, done counters from kCtlCounters + 2 kCtlItems, each region at a
+// fixed place whatever the shape.
 constexpr int kCtlCounters = 32;
-constexpr int kCtlItems = (int)((kCtlBytes / 4 - kCtlCounters) / 4) & ~1;
+constexpr int kCtlItems = (int)((kCtlBytes / 4 - kCtlCounters) / 3) & ~1;
+// Extra workgroups at the end of the fused backward's grid that run orphaned
+// dQ items (one per XCD).
+constexpr int kOrphanRunners = 8;
 
-// Per-launch parameters of the fused backward's dQ hand-over.
+// Per-launch parameters of the fused backward's dQ claims.
 struct FusedSync
 {
-    unsigned epoch;        // never 0; differs between consecutive launches on one control block
-    long long wait_ticks;  // wall-clock ticks (wall_clock64) a dQ wait may last
-    int need_extra;        // test hook: added to every awaited count (0 in normal use)
+    unsigned epoch;          // never 0; differs between consecutive launches on one control block
+    int n_main;              // main workgroups (the grid holds kOrphanRunners more)
+    int need_extra;          // test hook: added to every awaited count (0 in normal use)
+    long long wait_ticks;    // wall-clock ticks (wall_clock64) an owner waits before orphaning its item
+    long long safety_ticks;  // wall-clock ticks after which a runner's wait for an item's counts is an error
+    long long done_ticks;    // the same for a runner's wait for the main workgroups' decisions
 };
 
 // Backward, head_dim 64, fp32 MFMA, deterministic, one launch for T <= 256:
-// one dK/dV item per workgroup, then dQ items that start on each pair of
-// query blocks as soon as its dS tiles are complete. Correct whatever part of
-// the grid is resident; taken for grids one round of the CUs holds, needing
-// one chunk (bwd_fused_d64_fits). `ws` holds the dS tiles of all B * H (b, h),
-// `ctl` the control block; n_cu = compute units.
+// one dK/dV item per main workgroup, then the dQ of its diagonal blocks once
+// their dS tiles are complete (or, after a bounded wait, by an orphan runner).
+// Correct whatever part of the grid is resident; taken for grids one round
+// of the CUs holds, needing one chunk (bwd_fused_d64_fits). `ws` holds the dS
+// tiles of all B * H (b, h), `ctl` the control block; n_cu = compute units.
 bool bwd_fused_d64_fits(const Shape &s, int bh_per_chunk, int n_cu);
+int bwd_fused_d64_main_workgroups(const Shape &s);
 hipError_t launch_bwd_fused_d64(float *grad_x, float *D, const float *lse, const float *dy, const float *y,
                                 const float *qkv, float *ws, int *ctl, int n_cu, const FusedSync &sync,
                                 const Shape &s, hipStream_t st);

@@ -99,29 +99,32 @@ int gpt_hip_attn_bwd_f32_noalloc(float *grad_x, float *D_cache, const float *lse
                                  int batch_size, int seq_len, int hidden_size, int num_heads,
                                  void *stream);
 
-/* Number of dQ waits in the one-launch backward (T <= 256) that reached
- * their time limit, on the calling thread's current device, since the last
+/* Number of waits in the one-launch backward (T <= 256) that reached their
+ * safety time limit, on the calling thread's current device, since the last
  * call; the counts are cleared. Waits for all work queued on the device
- * first (hipDeviceSynchronize). A dQ item waits only for dK/dV work that has
- * already started on the GPU, which stores its dS tiles without waiting for
- * anything itself (work that has not started gets the dQ item handed over
- * instead), so any correct run returns 0 whatever else shares the GPU; a
+ * first (hipDeviceSynchronize). The owner of a dQ item waits for its dS tiles
+ * only a bounded time (about 50 us) and otherwise hands the item to extra
+ * workgroups at the end of the grid, which wait only for work that waits for
+ * nothing itself; so a correct run returns 0 whatever else shares the GPU. A
  * nonzero count means that many dQ items read incomplete tiles (wrong dQ
- * rows). A launch with such a wait still leaves the control block ready for
- * the next call. Returns the count (>= 0), or GPT_HIP_ATTN_ENODEV /
- * GPT_HIP_ATTN_ELAUNCH. No reference counterpart (the reference's dQ uses
- * atomics and never waits). */
+ * rows); when there was one, the control blocks are also cleared here, so
+ * that later calls start clean. Returns the count (>= 0), or
+ * GPT_HIP_ATTN_ENODEV / GPT_HIP_ATTN_ELAUNCH. No reference counterpart (the
+ * reference's dQ uses atomics and never waits). */
 int gpt_hip_attn_wait_timeouts(void);
 
 /* Test hook for the one-launch backward's dQ waits (process-wide, read at
- * each launch; not thread-safe). `microseconds` is the time limit of one
- * wait (default 1000000; a negative value restores it); `extra_need` is
- * added to every count a dQ item waits for (default 0), so that with
- * extra_need > 0 every wait that is not skipped runs to the limit: this is
- * how tests drive the timeout path without stalling the GPU. Results of a
- * launch made with extra_need > 0 are undefined (its waits time out); the
- * next launch with the defaults is correct. Returns 0, or
- * GPT_HIP_ATTN_EINVAL for extra_need < 0. No reference counterpart. */
+ * each launch; not thread-safe). `microseconds` limits the owners' wait
+ * before they hand an item over (default 50) and the wait of the workgroups
+ * that take handed-over items for those items' counts (a safety limit,
+ * default 1000000); a negative value restores both defaults. (Those
+ * workgroups' wait for every owner's decision keeps its one-second limit.) `extra_need` is added to every count
+ * a dQ item waits for (default 0), so that with extra_need > 0 every owner
+ * hands its item over and every taker's wait runs to the limit: this is how
+ * tests drive the timeout path without stalling the GPU. Results of a launch
+ * made with extra_need > 0 are undefined (its waits time out); the next
+ * launch with the defaults is correct. Returns 0, or GPT_HIP_ATTN_EINVAL for
+ * extra_need < 0. No reference counterpart. */
 int gpt_hip_attn_set_wait_limit(long long microseconds, int extra_need);
 
 /* Frees the default backward's dS workspaces on the calling thread's current

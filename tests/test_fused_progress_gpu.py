@@ -1,12 +1,13 @@
 """The one-launch backward (T <= 256) without whole-grid residency, and its
-wait time limit.
+wait time limits.
 
-A dQ item waits only for key groups whose workgroups have started, and hands
-its item to one that has not (gpt_amd/csrc/attn_bwd_fused.hip). These tests
-run it (1) with its waits forced to their time limit from the host, then
-again normally, and (2) while another stream's kernel holds half of the
-compute units, so that only part of the grid is resident at a time. Every
-call goes through the C ABI. The CPU model of the same protocol is
+The owner of a dQ item waits a bounded time for its dS tiles, then hands the
+item to extra workgroups at the end of the grid, which run it once every
+main workgroup has decided (gpt_amd/csrc/attn_bwd_fused.hip). These tests run
+it (1) with its waits forced to their limits from the host, then again
+normally, and (2) while another stream's kernel holds half of the compute
+units, so that only part of the grid is resident at a time. Every call goes
+through the C ABI. The CPU model of the same protocol is
 tests/test_dq_handoff_model.py.
 """
 import ctypes
@@ -52,13 +53,13 @@ ENTRIES = {
 @pytest.mark.parametrize("B", [8, 16])
 def test_wait_timeouts_are_counted_and_the_next_call_is_clean(dev, B, entry):
     """With every awaited count raised by one (a count that never arrives)
-    and a zero time limit, each dQ item of key groups 1..3 reaches its limit
-    exactly once (its owner's, or the claim of the key group it was handed
-    to): B * H * 3 timeouts, reported by gpt_hip_attn_wait_timeouts. The next
-    call with the defaults gives the clean call's bits again: the timed-out
-    launch left the control block ready (counters back at 0, marks and
-    mailboxes of an older epoch). B = 8 takes the kernel's half-grid
-    instantiation, B = 16 the full-grid one."""
+    and zero time limits, every owner of a dQ item of key groups 1..3 hands
+    its item over and the wait of the workgroup that takes it reaches its
+    limit: B * H * 3 expired waits, reported by gpt_hip_attn_wait_timeouts.
+    A call made right after with the defaults, before the count is read (and
+    the control block cleared), already gives the clean call's bits: the
+    timed-out launch left its counters at 0. B = 8 takes the kernel's
+    half-grid instantiation, B = 16 the full-grid one."""
     import torch
 
     fn = ENTRIES[entry]
@@ -70,16 +71,18 @@ def test_wait_timeouts_are_counted_and_the_next_call_is_clean(dev, B, entry):
     try:
         gpt_amd.set_wait_limit(0, 1)
         _bwd(fn, x, g, y, lse, B)
-        torch.cuda.synchronize()
     finally:
         gpt_amd.set_wait_limit(-1, 0)
-    n = gpt_amd.wait_timeouts()
-    print(f"B={B} {entry}: {n} timeouts with the forced limit", flush=True)
-    assert n == B * H * 3
     again, D1 = _bwd(fn, x, g, y, lse, B)
     torch.cuda.synchronize()
-    assert gpt_amd.wait_timeouts() == 0
     assert torch.equal(again, clean) and torch.equal(D1, D0)
+    n = gpt_amd.wait_timeouts()
+    print(f"B={B} {entry}: {n} expired waits with the forced limit", flush=True)
+    assert n == B * H * 3
+    third, D2 = _bwd(fn, x, g, y, lse, B)
+    torch.cuda.synchronize()
+    assert gpt_amd.wait_timeouts() == 0
+    assert torch.equal(third, clean) and torch.equal(D2, D0)
 
 
 def _occupier():

@@ -125,14 +125,17 @@ WAIT_VM = re.compile(r"^s_waitcnt\b.*\bvmcnt\((\d+)\)")
 
 def bump_order_violations(instrs):
     """Counter bumps of the fused backward's walk (the global_atomic_add
-    before the mailbox exchange) that do not follow, in program order, a
-    workgroup barrier with no vector store between the two, preceded since the
-    barrier before it by a vmcnt wait of at most 8 (what the kernel's dS
-    hand-over relies on: each wave waits for its earlier dS stores, the
-    barrier gathers the waves, then one thread bumps)."""
-    close = next((k for k, s in enumerate(instrs) if s.startswith("global_atomic_swap_x2")), None)
-    assert close is not None, "no mailbox exchange found"
-    bumps = [k for k, s in enumerate(instrs[:close]) if s.startswith("global_atomic_add ")]
+    between the walk's first v_mfma_f32_16x16x4_f32 and the s_setprio 0 that
+    ends it) that do not follow, in program order, a workgroup barrier with no
+    vector store between the two, preceded since the barrier before it by a
+    vmcnt wait of at most 8 (what the kernel's dS hand-over relies on: each
+    wave waits for its earlier dS stores, the barrier gathers the waves, then
+    one thread bumps)."""
+    start = next((k for k, s in enumerate(instrs) if s.startswith("v_mfma_f32_16x16x4")), None)
+    assert start is not None, "no walk found"
+    end = next((k for k in range(start, len(instrs)) if re.match(r"s_setprio\s+0\b", instrs[k])), None)
+    assert end is not None, "no end of the walk found"
+    bumps = [k for k in range(start, end) if instrs[k].startswith("global_atomic_add ")]
     bad = []
     for k in bumps:
         b = max((j for j in range(k) if instrs[j].startswith("s_barrier")), default=None)
@@ -171,15 +174,14 @@ def test_fused_backward_bumps_follow_the_store_wait_and_barrier():
 
 
 def test_bump_checker_flags_a_moved_atomic():
-    ok = ["global_store_dword v[1:2], v3, off sc1", "s_waitcnt vmcnt(8)", "s_barrier",
-          "global_atomic_add v[4:5], v6, off offset:128", "global_atomic_swap_x2 v[1:2], v0, v[2:3], s[0:1]"]
-    moved = ["global_store_dword v[1:2], v3, off sc1", "s_waitcnt vmcnt(8)",
-             "global_atomic_add v[4:5], v6, off offset:128", "s_barrier",
-             "global_atomic_swap_x2 v[1:2], v0, v[2:3], s[0:1]"]
-    sunk = ["s_waitcnt vmcnt(8)", "s_barrier", "global_store_dword v[1:2], v3, off sc1",
-            "global_atomic_add v[4:5], v6, off offset:128", "global_atomic_swap_x2 v[1:2], v0, v[2:3], s[0:1]"]
-    nowait = ["s_barrier", "global_store_dword v[1:2], v3, off sc1", "s_waitcnt vmcnt(12)", "s_barrier",
-              "global_atomic_add v[4:5], v6, off offset:128", "global_atomic_swap_x2 v[1:2], v0, v[2:3], s[0:1]"]
+    ok = ["v_mfma_f32_16x16x4_f32 v[0:3], v4, v5, v[0:3]", "global_store_dword v[1:2], v3, off sc1",
+          "s_waitcnt vmcnt(8)", "s_barrier", "global_atomic_add v[4:5], v6, off offset:128", "s_setprio 0"]
+    moved = ["v_mfma_f32_16x16x4_f32 v[0:3], v4, v5, v[0:3]", "global_store_dword v[1:2], v3, off sc1",
+             "s_waitcnt vmcnt(8)", "global_atomic_add v[4:5], v6, off offset:128", "s_barrier", "s_setprio 0"]
+    sunk = ["v_mfma_f32_16x16x4_f32 v[0:3], v4, v5, v[0:3]", "s_waitcnt vmcnt(8)", "s_barrier",
+            "global_store_dword v[1:2], v3, off sc1", "global_atomic_add v[4:5], v6, off offset:128", "s_setprio 0"]
+    nowait = ["v_mfma_f32_16x16x4_f32 v[0:3], v4, v5, v[0:3]", "s_barrier", "global_store_dword v[1:2], v3, off sc1",
+              "s_waitcnt vmcnt(12)", "s_barrier", "global_atomic_add v[4:5], v6, off offset:128", "s_setprio 0"]
     assert bump_order_violations(ok)[1] == []
     assert bump_order_violations(moved)[1]
     assert bump_order_violations(sunk)[1]
