@@ -30,7 +30,6 @@ except in two deliberately extreme tests, which pass a looser term of
 (dQ 2.6e-5, O 2.1e-6) and single rows of 32736 and 32800 keys checked against
 float64 (O 2.7e-6).
 """
-import os
 
 import numpy as np
 
@@ -77,7 +76,7 @@ def assert_close(name: str, x, r, rtol: float, elementwise: bool = True,
     print(f"{name}: rel_err {e:.3e} (<= {rtol:.0e}), elementwise excess {ex:.3e}"
           + (f" (<= {atol:.0e})" if elementwise else " (not gated)"))
     assert e <= rtol, f"{name}: rel_err {e:.3e} > {rtol:.0e} (elementwise excess {ex:.3e})"
-    if elementwise and not os.environ.get("GPT_AMD_ELEM_REPORT_ONLY"):
+    if elementwise:
         assert ex <= atol, (f"{name}: elementwise |x-r| > {rtol:.0e}|r| + {atol:.0e} max|r| "
                             f"(excess {ex:.3e})")
     return e
