@@ -36,30 +36,39 @@ from gpt_amd import synth  # noqa: E402
 
 S, V, VP, L, H, D, F = 64, 507, 512, 4, 4, 32, 256
 SEED = 4242
+# the gpt_test config as a mapping; the functions below take any such config
+GPT_TEST = dict(S=S, V=V, VP=VP, L=L, H=H, D=D, F=F)
 GELU_SQRT_2_OVER_PI = 0.79788456  # reference src/backend/cpu/cpu_backend.cpp:234
 GELU_CUBIC = 0.044715
 
-# (name, shape) in gpt_weights packing order
-LAYOUT = [
-    ("wte", (VP, D)), ("wpe", (S, D)),
-    ("ln_1_w", (L, D)), ("ln_1_b", (L, D)),
-    ("qkv_proj_w", (L, D, 3 * D)), ("qkv_proj_b", (L, 3 * D)),
-    ("attn_proj_w", (L, D, D)), ("attn_proj_b", (L, D)),
-    ("ln_2_w", (L, D)), ("ln_2_b", (L, D)),
-    ("ffn_up_w", (L, D, F)), ("ffn_up_b", (L, F)),
-    ("ffn_down_w", (L, F, D)), ("ffn_down_b", (L, D)),
-    ("ln_f_w", (D,)), ("ln_f_b", (D,)),
-]
+def layout(cfg):
+    """(name, shape) in gpt_weights packing order."""
+    S_, VP_, L_, D_, F_ = cfg["S"], cfg["VP"], cfg["L"], cfg["D"], cfg["F"]
+    return [
+        ("wte", (VP_, D_)), ("wpe", (S_, D_)),
+        ("ln_1_w", (L_, D_)), ("ln_1_b", (L_, D_)),
+        ("qkv_proj_w", (L_, D_, 3 * D_)), ("qkv_proj_b", (L_, 3 * D_)),
+        ("attn_proj_w", (L_, D_, D_)), ("attn_proj_b", (L_, D_)),
+        ("ln_2_w", (L_, D_)), ("ln_2_b", (L_, D_)),
+        ("ffn_up_w", (L_, D_, F_)), ("ffn_up_b", (L_, F_)),
+        ("ffn_down_w", (L_, F_, D_)), ("ffn_down_b", (L_, D_)),
+        ("ln_f_w", (D_,)), ("ln_f_b", (D_,)),
+    ]
+
+
+LAYOUT = layout(GPT_TEST)
 N_PARAMS = sum(int(np.prod(s)) for _, s in LAYOUT)
 
 
-def make_weights() -> np.ndarray:
+def make_weights(cfg=GPT_TEST, seed=SEED) -> np.ndarray:
     """N(0, 0.02) everywhere, LayerNorm gains 1 + N(0, 0.1), so that every
     parameter (biases included) carries a gradient path that depends on it."""
-    flat = synth.normal(SEED, (N_PARAMS,), std=0.02)
-    gains = synth.normal(SEED + 1, (N_PARAMS,), std=0.1)
+    lay = layout(cfg)
+    n_params = sum(int(np.prod(s)) for _, s in lay)
+    flat = synth.normal(seed, (n_params,), std=0.02)
+    gains = synth.normal(seed + 1, (n_params,), std=0.1)
     off = 0
-    for name, shape in LAYOUT:
+    for name, shape in lay:
         n = int(np.prod(shape))
         if name in ("ln_1_w", "ln_2_w", "ln_f_w"):
             flat[off:off + n] = (1.0 + gains[off:off + n]).astype(np.float32)
@@ -67,25 +76,28 @@ def make_weights() -> np.ndarray:
     return flat
 
 
-def make_tokens() -> np.ndarray:
-    u = synth.uniform(SEED + 2, S + 1)
-    return np.minimum((u * V).astype(np.int32), V - 1)
+def make_tokens(cfg=GPT_TEST, n=S + 1, seed=SEED) -> np.ndarray:
+    u = synth.uniform(seed + 2, n)
+    return np.minimum((u * cfg["V"]).astype(np.int32), cfg["V"] - 1)
 
 
-def unpack(flat, torch):
+def unpack(flat, torch, cfg=GPT_TEST):
     out, off = {}, 0
-    for name, shape in LAYOUT:
+    for name, shape in layout(cfg):
         n = int(np.prod(shape))
         out[name] = torch.tensor(flat[off:off + n].reshape(shape), dtype=torch.float64, requires_grad=True)
         off += n
     return out
 
 
-def loss_fn(w, tokens, torch):
+def loss_fn(w, tokens, torch, cfg=GPT_TEST, B=1, T=S):
+    """Mean cross-entropy over the B*T positions; inputs tokens[0:B*T] as B
+    rows of T, labels tokens[1:B*T+1] (the reference's gpt_test shift)."""
     F_ = torch.nn.functional
-    inp = torch.tensor(tokens[:S], dtype=torch.long)
-    lbl = torch.tensor(tokens[1:S + 1], dtype=torch.long)
-    d = D // H
+    V_, L_, H_, D_ = cfg["V"], cfg["L"], cfg["H"], cfg["D"]
+    inp = torch.tensor(tokens[:B * T], dtype=torch.long).reshape(B, T)
+    lbl = torch.tensor(tokens[1:B * T + 1], dtype=torch.long)
+    d = D_ // H_
 
     def ln(x, g, b):
         mean = x.mean(-1, keepdim=True)
@@ -95,29 +107,29 @@ def loss_fn(w, tokens, torch):
     def gelu(u):
         return 0.5 * u * (1.0 + torch.tanh(GELU_SQRT_2_OVER_PI * (u + GELU_CUBIC * u ** 3)))
 
-    mask = torch.triu(torch.ones(S, S, dtype=torch.bool), 1)
-    h = w["wte"][inp] + w["wpe"][:S]
-    for l in range(L):
+    mask = torch.triu(torch.ones(T, T, dtype=torch.bool), 1)
+    h = w["wte"][inp] + w["wpe"][:T]
+    for l in range(L_):
         qkv = ln(h, w["ln_1_w"][l], w["ln_1_b"][l]) @ w["qkv_proj_w"][l] + w["qkv_proj_b"][l]
-        q, k, v = (qkv[:, i * D:(i + 1) * D].reshape(S, H, d).transpose(0, 1) for i in range(3))
-        sc = (q @ k.transpose(1, 2)) / np.sqrt(d)
+        q, k, v = (qkv[..., i * D_:(i + 1) * D_].reshape(B, T, H_, d).transpose(1, 2) for i in range(3))
+        sc = (q @ k.transpose(-1, -2)) / np.sqrt(d)
         p = torch.softmax(sc.masked_fill(mask, float("-inf")), -1)
-        att = (p @ v).transpose(0, 1).reshape(S, D)
+        att = (p @ v).transpose(1, 2).reshape(B, T, D_)
         h = h + att @ w["attn_proj_w"][l] + w["attn_proj_b"][l]
         u = ln(h, w["ln_2_w"][l], w["ln_2_b"][l]) @ w["ffn_up_w"][l] + w["ffn_up_b"][l]
         h = h + gelu(u) @ w["ffn_down_w"][l] + w["ffn_down_b"][l]
     logits = ln(h, w["ln_f_w"], w["ln_f_b"]) @ w["wte"].t()
-    return F_.cross_entropy(logits[:, :V], lbl)
+    return F_.cross_entropy(logits[..., :V_].reshape(B * T, V_), lbl)
 
 
-def gradients(flat: np.ndarray, tokens: np.ndarray):
+def gradients(flat: np.ndarray, tokens: np.ndarray, cfg=GPT_TEST, B=1, T=S, as_float64=False):
     import torch
 
-    w = unpack(flat, torch)
-    loss = loss_fn(w, tokens, torch)
+    w = unpack(flat, torch, cfg)
+    loss = loss_fn(w, tokens, torch, cfg, B, T)
     loss.backward()
-    g = np.concatenate([w[name].grad.numpy().reshape(-1) for name, _ in LAYOUT]).astype(np.float32)
-    return float(loss.detach()), g
+    g = np.concatenate([w[name].grad.numpy().reshape(-1) for name, _ in layout(cfg)])
+    return float(loss.detach()), (g if as_float64 else g.astype(np.float32))
 
 
 def main(out_dir: str) -> None:

@@ -67,3 +67,22 @@ def test_planted_gelu_mistake_is_caught(tmp_path, monkeypatch):
     monkeypatch.setattr(mk, "GELU_CUBIC", 0.0)
     _, g_bad = mk.gradients(mk.make_weights(), mk.make_tokens())
     assert np.abs(g_bad - cpu).max() > 1e-5
+
+
+def test_d64_gradient_fixture_pins_the_restatement():
+    """tests/golden/gpt_d64/meta.json (written by make_gpt_d64_fixture.py from
+    the reference's own CPU backend and the float64 restatement at head_dim
+    64) holds every tensor's CPU-vs-float64 error at fp32 round-off level: the
+    restatement, which the head_dim-64 GPU check compares against, is the
+    reference model at that config too."""
+    import json
+
+    meta = json.load(open(os.path.join(ROOT, "tests", "golden", "gpt_d64", "meta.json")))
+    assert len(meta["tensors"]) == 16
+    for rec in meta["tensors"]:
+        assert 0 < rec["cpu_rel_err"] < 1e-5, rec
+    assert abs(meta["cpu_loss"] - meta["fp64_loss"]) < 1e-4
+    n = sum(r["size"] for r in meta["tensors"])
+    assert os.path.getsize(os.path.join(ROOT, "tests", "golden", "gpt_d64", "cpu_sample.bin")) == 4 * sum(
+        min(meta["sample"], r["size"]) for r in meta["tensors"])
+    assert n == 15160320
