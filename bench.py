@@ -6,6 +6,10 @@ H=12, head_dim=64, fp32, packed qkv [B, T, 3C]. One "step" runs the 12
 forwards in layer order then the 12 backwards in reverse order, through the
 C ABI (gpt_amd/libgpt_hip_attn.so), with every input already resident in HBM.
 
+Timing: W warm-up steps, then untimed steps until the GPU has been busy for
+--settle-ms (250 ms; its clocks rise over the first ~30 ms of load after
+idle, see SETTLE_MS), then exactly K timed steps between two events.
+
 value = algorithmic FLOPs / GPU time, FLOPs = 12 * 7 * B * H * d * T * (T+1)
 (QK^T and PV forward; S recompute, dP, dV, dK, dQ backward; causal pairs
 including the diagonal; exp and masking not counted).
@@ -64,6 +68,26 @@ PEAK_FP32_MFMA_TFLOPS = 157.3
 LAYERS, B, T, C, H = 12, 16, 256, 768, 12
 D_HEAD = C // H
 CONFIG_SEED = 1237  # 1234 + config index 3
+# The GPU's clocks rise over the first ~30 ms of sustained load after idle:
+# in a kernel trace of this workload the fused backward takes 60.9 us per
+# launch over the first 5 steps and 52.3 us from step 30 on, the forward
+# 28.5 -> 24.2 us. The timed steps start once the GPU has been busy this long.
+SETTLE_MS = 250.0
+
+
+def settle(step, ms):
+    """Runs `step` untimed, in groups of 5 with a synchronize after each,
+    until `ms` milliseconds have passed; returns (steps run, ms taken)."""
+    import torch
+
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(5):
+            step()
+        n += 5
+        torch.cuda.synchronize()
+    return n, (time.perf_counter() - t0) * 1e3
 
 
 def attn_flops(b, t, h, d, fwd=True, bwd=True):
@@ -135,6 +159,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="after the warm-up steps, keep running untimed steps until the GPU has been busy "
+                         "this long, so that the timed steps run at settled clocks (0: off)")
     ap.add_argument("--cpu-layers", type=int, default=12,
                     help="layers of the workload timed on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -396,7 +423,8 @@ def _cpu_leg(x, g, H, bwd, sample, gpu_out):
 def configs_bench(args):
     """BASELINE configs 1, 2, 4 and 5(a) (BASELINE.md "Results"): per config,
     the forward (C1) or forward + backward through the C ABI on resident
-    inputs, K calls back to back between two events (after 3 warm-up calls),
+    inputs, K calls back to back between two events (after 3 warm-up calls
+    and the clock-settling calls of settle()),
     value = algorithmic FLOPs / time per call; per-kernel averages from the
     library's launch timer in a second pass; the CPU baseline leg on a
     bounded sample, with the GPU outputs' errors on it."""
@@ -430,6 +458,7 @@ def configs_bench(args):
         for _ in range(3):
             call()
         torch.cuda.synchronize()
+        settle_steps, settle_ms = settle(call, args.settle_ms)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(reps):
@@ -457,6 +486,7 @@ def configs_bench(args):
             "config": {"workload": f"BASELINE config {name[1:]}: causal {'fwd+bwd' if bwd else 'fwd'}, "
                                    f"B={Bc} T={Tc} H={H} d={D_HEAD}", "flops_per_call": flops, "reps": reps},
             "ms_per_call": round(ms, 5),
+            "settle": {"calls": settle_steps, "ms": round(settle_ms, 1)},
             **({"bwd_path": args.bwd_path} if args.bwd_path else {}),
             "pct_fp32_mfma_peak": round(100 * tf / PEAK_FP32_MFMA_TFLOPS, 2),
             "kernels": {k: {"avg_us": round(1e3 * t / n, 3), "launches": n} for k, (t, n) in per_kernel.items()
@@ -758,6 +788,7 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    settle_steps, settle_ms = settle(step, args.settle_ms)
 
     # Timed region: exactly K steps between two events, nothing else recorded.
     start = torch.cuda.Event(enable_timing=True)
@@ -811,6 +842,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"steps": settle_steps, "ms": round(settle_ms, 1)},
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
