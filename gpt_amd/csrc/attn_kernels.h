@@ -74,7 +74,7 @@ hipError_t launch_bwd_d64(float *grad_x, float *D, const float *lse, const float
                           const float *qkv, float *ws, int bh_per_chunk, const Shape &s, hipStream_t st);
 
 // Control block of the one-launch fused backward (layout in
-// attn_bwd_fused.hip): a word of expired safety waits, then per (b, h, query
+// attn_bwd_fused_kernel.h): a word of expired safety waits, then per (b, h, query
 // block) a completion counter, per (b, h, key group) an orphan flag and per
 // (b, h) a done counter. It sits at the start of the workspace and is zeroed
 // when the workspace is allocated; every launch leaves its counters at 0,

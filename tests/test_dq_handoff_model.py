@@ -1,5 +1,5 @@
 """CPU model of the one-launch backward's dQ hand-over (gpt_amd/csrc/
-attn_bwd_fused.hip: the schedule at the end of bwd_fused_d64_kernel), run
+attn_bwd_fused_kernel.h: the schedule at the end of bwd_fused_d64_kernel), run
 under adversarial schedules.
 
 Main workgroups (one per key group J of a (b, h)) and orphan runners are

@@ -3,7 +3,7 @@ wait time limits.
 
 The owner of a dQ item waits a bounded time for its dS tiles, then hands the
 item to extra workgroups at the end of the grid, which run it once every
-main workgroup has decided (gpt_amd/csrc/attn_bwd_fused.hip). These tests run
+main workgroup has decided (gpt_amd/csrc/attn_bwd_fused_kernel.h). These tests run
 it (1) with its waits forced to their limits from the host, then again
 normally, and (2) while another stream's kernel holds half of the compute
 units, so that only part of the grid is resident at a time. Every call goes
