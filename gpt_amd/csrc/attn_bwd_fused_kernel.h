@@ -342,32 +342,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                     dk3 = mfma16(pa[r], qb.w, dk3);
                 }
             };
-            if constexpr (GEN)
-            {
-                if (kwe <= q0 + 31)
-                {
-                    if (kwe < q0 + 16)
-                    {
-                        if (!skip0)
-                            half(BufIdx<0>{});
-                    }
-                    else
-                    {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            store_sc1(tile + r * 32, 0.f);
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                    if (!skip1)
-                        half(BufIdx<1>{});
-                    __builtin_amdgcn_sched_barrier(0);
-                    vm_wait<8>();
-                }
-                else
-                    lds_dma_wait();
-            }
-            else
-            {
+            // Both 16-query halves of the block at once, four interleaved
+            // accumulator chains (S and dP of each half); MASK applies the
+            // causal mask, for a diagonal block where this wave has units in
+            // both halves.
+            auto four = [&](auto mask_c) {
+                constexpr bool MASK = decltype(mask_c)::value;
                 v4f s0 = zero4(), s1 = zero4(), p0 = zero4(), p1 = zero4();
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
@@ -405,6 +385,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                         s1[r] = pb;
                         p1[r] = pb * (p1[r] - d1v[r]);
                     }
+                    if (MASK)
+                    {
+                        const int key = kwe + c16;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                        {
+                            if (key > q0 + 4 * g4 + r)
+                                s0[r] = p0[r] = 0.f;
+                            if (key > q0 + 16 + 4 * g4 + r)
+                                s1[r] = p1[r] = 0.f;
+                        }
+                    }
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
@@ -434,7 +426,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 vm_wait<8>();
+            };
+            if constexpr (GEN)
+            {
+                // A wave with units in both halves runs them as one step
+                // (full grids: 12-layer C3 step 0.9189 / 0.9184 vs 0.9215 /
+                // 0.9209 ms, outputs bitwise unchanged); the HELP instantiation
+                // keeps the half-by-half form (with this form it spilled a
+                // VGPR and lost 1 % at B = 8).
+                if (!HELP && kwe < q0 + 16)
+                {
+                    if constexpr (!HELP)
+                        four(BufIdx<1>{});
+                }
+                else if (kwe <= q0 + 31)
+                {
+                    if (kwe < q0 + 16)
+                    {
+                        if (!skip0)
+                            half(BufIdx<0>{});
+                    }
+                    else
+                    {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            store_sc1(tile + r * 32, 0.f);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (!skip1)
+                        half(BufIdx<1>{});
+                    __builtin_amdgcn_sched_barrier(0);
+                    vm_wait<8>();
+                }
+                else
+                    lds_dma_wait();
             }
+            else
+                four(BufIdx<0>{});
             if constexpr (FUSE_D)
             {
                 if (i - 1 >= i_lo)
