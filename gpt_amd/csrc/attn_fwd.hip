@@ -360,7 +360,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(3))) vo
 // Workgroups are ordered heaviest first (J descending), (b, h) fastest; when
 // the whole grid is resident the middle round is reversed (in blocks of 8, one
 // XCD per (b, h)) so that every CU gets one heavy, one light and one middle
-// group.
+// group; grids of 1 to 2 workgroups per CU pair them (paired_item).
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void fwd_qs_d64_kernel(
     float *__restrict__ y, float *__restrict__ lse, const float *__restrict__ qkv, int T, int C, int H, int BH,
     int n_qg, float c2, int n_cu)
@@ -380,8 +380,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
             item = r * n_cu + c;
         }
     }
-    const int J = n_qg - 1 - item / BH;
-    const int bh = item % BH;
+    int J = n_qg - 1 - item / BH;
+    int bh = item % BH;
+    {
+        int cls = 0, idx = 0;
+        if (paired_item((int)blockIdx.x, (int)gridDim.x, n_cu, BH, &cls, &idx))
+        {
+            J = n_qg - 1 - cls;
+            bh = idx;
+        }
+    }
     const int b = bh / H, h = bh % H;
     const int qw0 = 64 * J + 16 * w;
     const uint32_t Wb = 12u * (uint32_t)C, Cb = 4u * (uint32_t)C;
