@@ -97,6 +97,20 @@ def test_config2_fwd_bwd_B8_T256(dev):
     print("C2 errors", errs)
 
 
+@pytest.mark.parametrize("B,T,C,H", [(6, 256, 768, 12), (10, 256, 768, 12), (16, 200, 512, 8), (24, 128, 512, 8),
+                                     (16, 160, 512, 8)])
+def test_paired_grids_fwd_bwd(dev, B, T, C, H):
+    """Grids of 1 to 2 workgroups per CU (on 256 CUs: 288, 480, 512 and 384
+    workgroups of 4, 4, 4, 2 and 3 item classes) take the paired layout
+    (paired_item: the heaviest items alone on their CUs, the others paired
+    heavy with light), in the forward and in the one-launch backward: every
+    output against the oracle, which fails if an item were lost or run
+    twice."""
+    x = synth.qkv(B, T, C, seed=700 + B + T)
+    g = synth.grad_out(B, T, C, seed=700 + B + T)
+    check_fwd_bwd(dev, x, g, H, tag=f"paired B={B} T={T} H={H}")
+
+
 @pytest.mark.parametrize("T", [1, 2, 3, 31, 32, 33, 63, 64, 65, 95, 127, 128, 129, 191, 255, 257, 300])
 def test_ragged_T_fwd_bwd(dev, T):
     B, C, H = 2, 192, 3
