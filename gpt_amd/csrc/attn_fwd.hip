@@ -606,18 +606,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
 
     // register r of accumulator e: O[qw0 + c16][16 g4 + 4 r + e]
     l = halves_sum(rows16_sum(l));
-    const int row = qw0 + c16;
-    if (row < T)
+    const float inv = 1.f / l;
     {
-        const float inv = 1.f / l;
-        float *dst = y + ((long)b * T + row) * C + (long)h * 64 + 16 * g4;
+        // The wave's 16 x 64 O tile goes through LDS (the K/V buffers are
+        // free after the last block's barrier: one buffer per wave, rows of
+        // 68 words), so that each store instruction writes 4 whole 256-byte
+        // rows, and the rows are written through to memory (device scope,
+        // sc1). Lines left dirty in the XCD's L2 would be written back when
+        // the launch ends, after the last workgroup: C3 forward 24.1 ->
+        // 21.8 us (23.5 us with the staging alone).
+        float *stg = w == 0 ? sk0 : w == 1 ? sv0 : w == 2 ? sk1 : sv1;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            *reinterpret_cast<float4 *>(dst + 4 * r) =
+            *reinterpret_cast<float4 *>(stg + c16 * 68 + 16 * g4 + 4 * r) =
                 make_float4(o0[r] * inv, o1[r] * inv, o2[r] * inv, o3[r] * inv);
-        if (g4 == 0)
-            lse[((long)b * T + row) * H + h] = (m + fast_log2(l)) * kLn2;
+        const rsrc_t ry =
+            make_rsrc(y + (long)b * T * C + (long)h * 64, (uint32_t)(((long)T * C - (long)h * 64) * 4));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const int rr = (lane >> 4) + 4 * i;
+            const float4 v = *reinterpret_cast<const float4 *>(stg + rr * 68 + 4 * (lane & 15));
+            if (qw0 + rr < T)
+                store4_sc1(ry, (uint32_t)(qw0 + rr) * 4u * (uint32_t)C + 16u * (uint32_t)(lane & 15), v);
+        }
     }
+    const int row = qw0 + c16;
+    if (row < T && g4 == 0)
+        lse[((long)b * T + row) * H + h] = (m + fast_log2(l)) * kLn2;
 }
 
 // Split-key head_dim-64 forward for calls too small to fill the GPU with
