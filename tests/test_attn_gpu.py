@@ -591,3 +591,41 @@ def test_launch_timer_counts_each_kernel(dev, T):
     for k in set(gpt_amd.attention.KERNEL_KINDS) - set(kinds):
         assert t[k] == (0.0, 0), (k, t[k])
     assert gpt_amd.timing_read()["fwd"] == (0.0, 0)  # read forgets
+
+
+@pytest.mark.parametrize("B,T", [(16, 255), (16, 200), (3, 257), (1, 100)])
+def test_outputs_stay_in_their_buffers(dev, B, T):
+    """Every output written only inside its tensor: y, lse, grad_x and D are
+    views into buffers with 1024-float guard bands on both sides, filled with
+    a bit pattern no kernel writes; after the forward and the backward the
+    guards are unchanged and the outputs match the oracle. The shapes take
+    the Q-stationary forward with ragged rows and the one-launch backward
+    (B = 16), and the smaller-grid forwards and the two-launch backward."""
+    import torch
+
+    C, H, G = 768, 12, 1024
+    x = synth.qkv(B, T, C, 61)
+    g = synth.grad_out(B, T, C, 61)
+    xd, gd = _to(dev, x), _to(dev, g)
+    pat = -12345.678
+
+    def guarded(n):
+        buf = torch.full((G + n + G,), pat, dtype=torch.float32, device=dev)
+        return buf, buf[G:G + n]
+
+    ybuf, y = guarded(B * T * C)
+    lbuf, lse = guarded(B * T * H)
+    gbuf, gx = guarded(B * T * 3 * C)
+    dbuf, D = guarded(B * T * H)
+    gpt_amd.attention.device_flash_attention_forward(y, lse, xd, B, T, C, H)
+    gpt_amd.attention.device_flash_attention_backward(gx, D, lse, gd, y, xd, B, T, C, H)
+    torch.cuda.synchronize()
+    for name, buf in (("y", ybuf), ("lse", lbuf), ("grad_x", gbuf), ("D", dbuf)):
+        guards = torch.cat([buf[:G], buf[-G:]])
+        assert bool(torch.all(guards == pat)), f"{name}: a guard band was written"
+    yr, lr = pyoracle.forward(x, H)
+    assert_close(f"B={B} T={T} O", y.view(B, T, C).cpu().numpy(), yr, FWD_RTOL)
+    assert_close(f"B={B} T={T} LSE", lse.view(B, T, H).cpu().numpy(), lr, FWD_RTOL)
+    gr, Dr = pyoracle.backward(x, y.view(B, T, C).cpu().numpy(), lse.view(B, T, H).cpu().numpy(), g, H)
+    assert_close(f"B={B} T={T} dQKV", gx.view(B, T, 3 * C).cpu().numpy(), gr, BWD_RTOL)
+    assert_close(f"B={B} T={T} D", D.view(B, T, H).cpu().numpy(), Dr, BWD_RTOL)
