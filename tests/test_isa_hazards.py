@@ -186,3 +186,30 @@ def test_bump_checker_flags_a_moved_atomic():
     assert bump_order_violations(moved)[1]
     assert bump_order_violations(sunk)[1]
     assert bump_order_violations(nowait)[1]
+
+
+def test_forward_output_rows_are_written_through():
+    """The Q-stationary forward writes its O rows with 16-byte device-scope
+    (sc1) buffer stores and no other 16-byte store. Lines left dirty in the
+    XCD's L2 are written back after the launch's last workgroup (measured:
+    2.4 us per C3 forward), so a plain store here would be a silent
+    regression."""
+    lib = LIBS[0]
+    if not os.path.exists(lib):
+        pytest.skip("library not built")
+    import tempfile
+
+    found = 0
+    with tempfile.TemporaryDirectory() as d:
+        for k, obj in enumerate(gfx950_code_objects(lib)):
+            f = os.path.join(d, f"co{k}.o")
+            open(f, "wb").write(obj)
+            asm = subprocess.run([OBJDUMP, "-d", "--mcpu=gfx950", f], capture_output=True, text=True,
+                                 check=True).stdout
+            for name, instrs in kernel_bodies(asm, "fwd_qs_d64_kernel").items():
+                x4 = [s for s in instrs if re.match(r"(global|buffer|flat)_store_dwordx4\b", s)]
+                assert x4, (name, "no 16-byte store")
+                plain = [s for s in x4 if not s.startswith("buffer_store_dwordx4") or not re.search(r"\bsc1\b", s)]
+                assert not plain, (name, plain[:4])
+                found += 1
+    assert found == 1
