@@ -391,6 +391,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
         }
     }
     const int b = bh / H, h = bh % H;
+    if (J == 0 && n_qg == 4 && (int)gridDim.x > 2 * n_cu && (int)gridDim.x <= 3 * n_cu)
+    {
+        // Whole grid resident at 3 per CU (C3): the J = 0 workgroups are the
+        // youngest on their CUs and get no MFMA time until about 13 us in,
+        // while every workgroup's Q and first K/V arrive at once from HBM.
+        // Their first loads wait about 3.4 us (127 x 64 cycles), so that
+        // the heavier groups' start-up data arrives first: C3 forward
+        // 21.62-21.78 -> 21.37-21.45 us (A/B on one box, outputs unchanged;
+        // 1.7 us: 21.54-21.58 us, 6.8 us: no gain).
+        __builtin_amdgcn_s_sleep(127);
+    }
     const int qw0 = 64 * J + 16 * w;
     const uint32_t Wb = 12u * (uint32_t)C, Cb = 4u * (uint32_t)C;
     const rsrc_t rs = make_rsrc(qkv + (long)b * T * 3L * C + (long)h * 64,
